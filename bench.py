@@ -1,0 +1,236 @@
+"""Decode throughput of the Qwen3-8B-shape Q4_0 token loop on one MI355X.
+
+Workload (one step = one greedy decode token): Qwen3-8B shape (hidden 4096,
+36 layers, 32/8 heads x 128, intermediate 12288, vocab 151936), Q4_0 linear
+weights of seeded synthetic values, tied Q4 LM head, f16 KV cache pre-filled
+with 4096 positions of N(0,1), batch 1.  Timed: K decode steps from position
+4096 (HIP-graph replay of the device-resident step), inputs resident in HBM.
+
+Prints one JSON line.  Extra fields: the Q4 GEMV roofline (HIP events on the
+library stream over profiled decode steps), the CPU oracle baseline on a
+bounded sample, and the Qwen3-0.6B-shape token loop.
+
+  python bench.py [--steps K] [--warmup W] [--gpus 1]
+"""
+import argparse
+import json
+import os
+import platform
+import subprocess
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "chat-wgpu_amd"))
+import cw  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+PRE = 4096
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def q4_bytes(out_f, in_f):
+    return out_f * (in_f // 32) * 18
+
+
+def gemv_bytes_per_token(cfg):
+    """Algorithmic bytes of one token's Q4 GEMV launches: weights (18 B per 32)
+    + activation read (K f32) + output write (N f32) per launch."""
+    q, kv, d, h, v = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim, cfg.dim, \
+        cfg.hidden, cfg.vocab
+    per_layer = [
+        (q + 2 * kv, d, 1),  # fused RMSNorm + QKV
+        (d, q, 2),           # O + residual (reads residual too)
+        (2 * h, d, 0),       # gate/up pair (+SwiGLU): 2h rows, writes h
+        (d, h, 2),           # down + residual
+    ]
+    total = 0
+    for n, k, extra in per_layer:
+        w = q4_bytes(n, k)
+        out_n = h if n == 2 * h else n
+        total += w + 4 * k + 4 * out_n + (4 * n if extra == 2 else 0)
+    total *= cfg.n_layers
+    total += q4_bytes(v, d) + 4 * d + 4 * v
+    weights = cfg.n_layers * (q4_bytes(q + 2 * kv, d) + q4_bytes(d, q) + q4_bytes(2 * h, d) +
+                              q4_bytes(d, h)) + q4_bytes(v, d)
+    return total, weights
+
+
+def kv_bytes_per_token(cfg, seq, es):
+    return cfg.n_layers * seq * cfg.n_kv_heads * cfg.head_dim * 2 * es
+
+
+def cpu_info():
+    model = platform.processor() or ""
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return model, os.cpu_count()
+
+
+def profile_gemv(ctx, model, n_steps):
+    """Per-kernel HIP-event timings over n_steps eager decode steps."""
+    ctx.profile_begin()
+    model.decode_async(n_steps, use_graph=False)
+    rows = ctx.profile_report()
+    return {name: (count / n_steps, ms / n_steps) for name, count, ms in rows}
+
+
+def cpu_baseline_8b(cfg, weights, k, v, start_tok, budget_s):
+    """The CPU oracle (C restatement of the reference forward, single thread)
+    on decode tokens from position 4096 until budget_s has elapsed."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    orc.set_threads(1)
+    o = orc.OracleModel(cfg, weights)
+    o.prefill_kv(k, v, PRE)
+    tok, n, t0 = int(start_tok), 0, time.perf_counter()
+    while True:
+        logits, _ = o.step(tok, PRE + n)
+        tok = int(np.argmax(logits))
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 8:
+            break
+    o.close()
+    return n / el, n, el
+
+
+def bench_06b(ctx, warm=True):
+    P, N = 32, 128
+    cfg = cw.make_config(28, 1024, 16, 8, 128, 3072, 151936, P + N, cw.CW_F32, 1e-6, 1e6)
+    m = cw.Model(ctx, cfg)
+    m.load_synthetic(2024)
+    m.finalize()
+    prompt = cw.synth_tokens(cw.synth_key(2024, "prompt"), P, cfg.vocab)
+    if warm:
+        m.generate(prompt, N, use_graph=True)
+    t0 = time.perf_counter()
+    m.generate(prompt, N, use_graph=True)
+    el = time.perf_counter() - t0
+    m.close()
+    return (P + N - 1) / el, el
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
+                          "(no multi-GPU path is built)"}))
+        sys.exit(2)
+    K, W = args.steps, args.warmup
+
+    ctx = cw.Context(0)
+    info = ctx.info()
+    log(f"device {info}")
+    cfg = cw.make_config(36, 4096, 32, 8, 128, 12288, 151936, PRE + max(K, W), cw.CW_F16,
+                         1e-6, 1e6)
+    t = time.perf_counter()
+    weights = cw.synthetic_weights(cfg, 8008)
+    log(f"synthetic weights generated in {time.perf_counter() - t:.1f}s")
+    m = cw.Model(ctx, cfg)
+    m.set_weights(weights)
+    m.finalize()
+    kv_n = cfg.n_layers * PRE * cfg.n_kv_heads * cfg.head_dim
+    k = cw.synth_normal_f16(cw.synth_key(8008, "kv.k"), kv_n)
+    v = cw.synth_normal_f16(cw.synth_key(8008, "kv.v"), kv_n)
+    m.prefill_kv(k, v, PRE)
+    start = int(cw.synth_tokens(cw.synth_key(8008, "start"), 1, cfg.vocab)[0])
+    log(f"model ready in {time.perf_counter() - t:.1f}s")
+
+    m.reset_state(start, PRE)
+    m.decode_async(W, use_graph=True)
+    ctx.flush()
+    log("warmup done")
+
+    m.reset_state(start, PRE)
+    ctx.flush()
+    t0 = time.perf_counter()
+    m.decode_async(K, use_graph=True)
+    ctx.flush()
+    el = time.perf_counter() - t0
+    toks = m.tokens(K)
+    tok_s = K / el
+    log(f"timed {K} steps in {el * 1e3:.2f} ms -> {tok_s:.1f} tok/s; first tokens {toks[:8]}")
+
+    # roofline of the dominant kernel family (Q4 GEMV) over profiled eager steps
+    m.reset_state(start, PRE)
+    prof = profile_gemv(ctx, m, 8)
+    gemv_ms = sum(ms for name, (_, ms) in prof.items() if name.startswith("q4_gemv"))
+    gemv_launches = sum(c for name, (c, _) in prof.items() if name.startswith("q4_gemv"))
+    gbytes, wbytes = gemv_bytes_per_token(cfg)
+    achieved = gbytes / (gemv_ms * 1e-3) / 1e9
+    kernel_ms = sum(ms for _, (_, ms) in prof.items())
+    log("per-token kernel ms: " + ", ".join(f"{n}={ms:.3f}" for n, (_, ms) in prof.items()))
+
+    result = {
+        "metric": "decode tokens/s (Qwen3-0.6B/8B Q4_0, 1 GPU); Q4 GEMV HBM GB/s vs peak",
+        "value": round(tok_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(el * 1e3 / K, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded Q4_0 weights, N(0,1) f16 KV pre-fill)",
+        "config": {"workload": "qwen3-8b-shape q4_0 greedy decode, batch 1, KV 4096->"
+                               f"{PRE + K} f16, {K} steps, hipGraph step replay",
+                   "weights": "q4_0", "hidden": 4096, "layers": 36, "heads": "32/8x128",
+                   "intermediate": 12288, "vocab": 151936, "kv_prefill": PRE,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "kernel": "q4_gemv* (all Q4 GEMV launches of one token)",
+                     "algorithmic_bytes_per_token": gbytes,
+                     "gemv_ms_per_token": round(gemv_ms, 4),
+                     "gemv_launches_per_token": gemv_launches},
+        "token_roofline": {
+            "bytes_per_token": wbytes + kv_bytes_per_token(cfg, PRE + K // 2, 2),
+            "ideal_ms": round((wbytes + kv_bytes_per_token(cfg, PRE + K // 2, 2)) /
+                              (HBM_PEAK_GBS * 1e6), 4),
+            "kernel_ms_per_token": round(kernel_ms, 4)},
+    }
+
+    if not args.no_cpu_baseline:
+        log("cpu baseline (oracle, 1 thread) ...")
+        tps, n, cel = cpu_baseline_8b(cfg, weights, k, v, start, args.cpu_budget)
+        model_name, ncpu = cpu_info()
+        result["cpu_baseline"] = {"value": round(tps, 5), "unit": "tokens/s", "cores": 1,
+                                  "kind": "port",
+                                  "sample": f"{n} decode tokens of the same 8B workload from "
+                                            f"position 4096 on the C oracle ({cel:.1f}s); "
+                                            f"host {model_name}, {ncpu} cpus"}
+    del weights
+    m.close()
+
+    if not args.no_extras:
+        tps06, el06 = bench_06b(ctx)
+        result["extras"] = {"qwen3_0.6b_token_loop_tok_s": round(tps06, 1),
+                            "qwen3_0.6b_token_loop": "32 prompt + 128 greedy, f32 KV, "
+                                                     "159 forwards incl. prompt"}
+    ctx.close()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,175 @@
+// Internal declarations shared by the HIP translation units of libchatwgpu.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "chat_wgpu.h"
+
+namespace cwi {
+
+void set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+int hip_fail(hipError_t e, const char *what, const char *file, int line);
+
+}  // namespace cwi
+
+#define CW_HIP(call)                                                         \
+    do {                                                                     \
+        hipError_t cw_e_ = (call);                                           \
+        if (cw_e_ != hipSuccess) return cwi::hip_fail(cw_e_, #call, __FILE__, __LINE__); \
+    } while (0)
+
+#define CW_CHECK_ARG(cond, ...)          \
+    do {                                 \
+        if (!(cond)) {                   \
+            cwi::set_error(__VA_ARGS__); \
+            return CW_ERR_ARG;           \
+        }                                \
+    } while (0)
+
+#define CW_TRY(expr)                   \
+    do {                               \
+        int cw_rc_ = (expr);           \
+        if (cw_rc_ != CW_OK) return cw_rc_; \
+    } while (0)
+
+// One profiled launch: events bracketing it and its label.
+struct cw_prof_rec {
+    hipEvent_t start, stop;
+    const char *label;
+};
+
+// A RoPE angle table resident on the device: cos/sin [max_pos][hd/2] f32.
+struct cw_rope_tab {
+    float theta;
+    int head_dim;
+    int max_pos;
+    float *cos_t;
+    float *sin_t;
+};
+
+struct cw_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int n_cu = 0;
+    size_t hbm_bytes = 0;
+    std::string arch;
+
+    // persistent allocations (freed at destroy)
+    std::vector<void *> allocs;
+
+    // per-frame arena: chunks handed out in call order, rewound by reset
+    struct Chunk {
+        char *base;
+        size_t size;
+    };
+    std::vector<Chunk> chunks;
+    size_t chunk_idx = 0, chunk_off = 0;
+
+    // kernel scratch (attention partials, argmax partials, counters) for the
+    // standalone kernel entry points; grows on demand between launches
+    void *scratch = nullptr;
+    size_t scratch_size = 0;
+
+    std::vector<cw_rope_tab> ropes;
+
+    // profiling
+    bool profiling = false;
+    std::vector<cw_prof_rec> prof;
+    std::vector<hipEvent_t> event_pool;
+    size_t event_next = 0;
+};
+
+namespace cwi {
+
+// Scratch of at least `bytes` for the standalone kernels (synchronises the
+// stream before it replaces a smaller buffer).
+int ctx_scratch(cw_ctx *ctx, size_t bytes, void **out);
+// Device RoPE table covering positions [0, min_pos) for (theta, head_dim).
+int ctx_rope_table(cw_ctx *ctx, float theta, int head_dim, int min_pos, const cw_rope_tab **out);
+// Build the host table (f64 angles rounded to f32), layout [pos][hd/2].
+void rope_table_host(int max_pos, int head_dim, float theta, float *cos_t, float *sin_t);
+
+// Profiling hooks around a launch (no-ops unless profiling).
+void prof_begin(cw_ctx *ctx, const char *label);
+void prof_end(cw_ctx *ctx);
+// Check the launch that was just enqueued.
+int launch_check(const char *what);
+
+// f16 helpers on the host (IEEE binary16, round to nearest even).
+uint16_t f32_to_f16_bits(float f);
+float f16_bits_to_f32(uint16_t h);
+
+// ---- kernel launchers (all enqueue on ctx->stream) ----
+
+enum XSrc { XS_PLAIN = 0, XS_RMSNORM = 1 };
+enum Epi { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2 };
+
+struct GemvArgs {
+    const float *x;         // activation [K] (raw hidden for XS_RMSNORM)
+    const float *norm_w;    // XS_RMSNORM gain [K]
+    float eps;
+    const uint16_t *sA;     // scales of matrix A [N][K/32]
+    const uint8_t *qA;      // quants of matrix A [N][K/32][16]
+    const uint16_t *sB;     // EPI_SWIGLU: the up matrix
+    const uint8_t *qB;
+    const float *resid;     // EPI_ADD
+    float *y;               // [N]
+    int K, N;
+};
+
+int launch_q4_gemv(cw_ctx *ctx, XSrc xs, Epi epi, const GemvArgs &a);
+
+// Attention: fused q/k-norm + RoPE + KV write + split-sequence partial
+// softmax + merge.
+struct AttnArgs {
+    const float *q;        // [n_heads*hd] (already normed/rotated) if qkv == null
+    const float *qkv;      // fused path: raw [q | k | v] GEMV output
+    const float *q_norm_w; // fused path gains [hd]
+    const float *k_norm_w;
+    float eps;
+    const float *cos_t, *sin_t;  // fused path RoPE table [max_pos][hd/2]
+    void *k_cache, *v_cache;     // [max_seq][n_kv*hd]
+    int kv_dtype;
+    int n_heads, n_kv, hd;
+    int seq;                // used when pos_dev == null
+    const int *pos_dev;     // device position; seq = pos+1 (fused path writes KV at pos)
+    int max_seq;            // grid sizing (positions the cache can hold)
+    float *out;             // [n_heads*hd]
+    float *part;            // scratch partials
+    unsigned *counters;     // [n_kv] zero-initialised, self-resetting
+};
+
+size_t attn_scratch_floats(int n_heads, int n_kv, int hd, int max_seq);
+int launch_attention(cw_ctx *ctx, const AttnArgs &a);
+
+int launch_rmsnorm(cw_ctx *ctx, const float *x, const float *w, int rows, int dim, float eps,
+                   float *y);
+int launch_rope(cw_ctx *ctx, const float *x, int rows, int hd, int pos, const float *cos_t,
+                const float *sin_t, float *y);
+int launch_add(cw_ctx *ctx, const float *a, const float *b, int n, float *c);
+int launch_swiglu(cw_ctx *ctx, const float *g, const float *u, int n, float *out);
+int launch_kv_write(cw_ctx *ctx, void *kc, void *vc, int kv_dtype, int pos, const int *pos_dev,
+                    int kv_dim, const float *k, const float *v);
+int launch_embed(cw_ctx *ctx, const float *table, int vocab, int dim, const uint32_t *tok_dev,
+                 float *out);
+
+// Argmax: stage 1 over blocks, stage 2 merge.  When `state` is non-null the
+// merge also advances the device-resident generate state.
+struct GenState {
+    int pos;          // position of the next forward
+    uint32_t token;   // token fed at pos
+    int start_pos;    // position of the first forward of this generate call
+    int n_prompt;
+    int produced;
+    int max_out;
+};
+size_t argmax_scratch_bytes(int n);
+int launch_argmax(cw_ctx *ctx, const float *logits, int n, uint32_t *out_dev, void *scratch,
+                  GenState *state, const uint32_t *prompt_dev, uint32_t *tokens_out_dev);
+
+}  // namespace cwi

@@ -1,0 +1,582 @@
+// Qwen3 decode model and the greedy token loop.
+//
+// Replaces Qwen3::load/forward/logits (src/model/qwen3.rs:44-191), KvCache
+// (src/model/cache.rs), Q4Linear/Proj/RmsNorm (src/model/layers.rs:74-191)
+// and model::generate (src/model/mod.rs:57-125).
+//
+// One decode step is 2 + 6 * n_layers launches on one stream:
+//   embed (token read on the device)
+//   per layer: RMSNorm+QKV GEMV | QK-norm+RoPE+KV write+attention partials |
+//              attention merge | O GEMV + residual | RMSNorm+gate/up GEMV+SwiGLU |
+//              down GEMV + residual
+//   final RMSNorm + LM head GEMV | argmax (advances the device generate state)
+// Position and token live in device memory, so the same launch sequence is
+// valid for every token and is captured once as a HIP graph and replayed
+// (the reference keeps "the same op sequence every token", mod.rs:78-81).
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "cw_internal.hpp"
+
+using namespace cwi;
+
+namespace {
+
+struct Q4W {
+    uint16_t *s = nullptr;
+    uint8_t *q = nullptr;
+    int out_f = 0, in_f = 0;
+};
+
+struct Layer {
+    float *attn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *ffn_norm = nullptr;
+    Q4W qkv, wo, gate, up, down;
+};
+
+// tensor ids within a layer
+enum { T_ATTN_NORM, T_Q_NORM, T_K_NORM, T_FFN_NORM, T_Q, T_K, T_V, T_O, T_GATE, T_UP, T_DOWN, T_N };
+const char *kLayerNames[T_N] = {"attn_norm", "attn_q_norm", "attn_k_norm", "ffn_norm", "attn_q",
+                                "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up",
+                                "ffn_down"};
+
+}  // namespace
+
+struct cw_model {
+    cw_ctx *ctx = nullptr;
+    cw_model_config cfg{};
+    int q_dim = 0, kv_dim = 0;
+    std::vector<Layer> layers;
+    std::vector<std::vector<bool>> have;  // [layer][T_N]
+    bool have_embed = false, have_final = false, have_output = false;
+    float *embed = nullptr, *final_norm = nullptr;
+    Q4W lm_head;
+    void *kcache = nullptr, *vcache = nullptr;  // [L][max_seq][kv_dim]
+    size_t kv_layer_bytes = 0;
+    const float *cos_t = nullptr, *sin_t = nullptr;
+    float *hidden = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
+    float *hidden_out = nullptr;
+    float *part = nullptr;
+    void *argmax_scratch = nullptr;
+    GenState *state = nullptr;
+    uint32_t *prompt_dev = nullptr, *tokens_dev = nullptr, *argmax_out = nullptr;
+    bool finalized = false;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+    std::vector<void *> allocs;
+};
+
+namespace {
+
+int dalloc(cw_model *m, size_t bytes, void **out) {
+    void *p = nullptr;
+    CW_HIP(hipMalloc(&p, bytes));
+    m->allocs.push_back(p);
+    *out = p;
+    return CW_OK;
+}
+
+int alloc_q4(cw_model *m, Q4W &w, int out_f, int in_f) {
+    w.out_f = out_f;
+    w.in_f = in_f;
+    const size_t nblk = (size_t)out_f * (in_f / 32);
+    CW_TRY(dalloc(m, nblk * 2, (void **)&w.s));
+    CW_TRY(dalloc(m, nblk * 16, (void **)&w.q));
+    return CW_OK;
+}
+
+int upload_rows(cw_model *m, Q4W &w, int row0, int rows, const uint16_t *s, const uint8_t *q) {
+    const size_t nb = w.in_f / 32;
+    CW_HIP(hipMemcpy(w.s + (size_t)row0 * nb, s, (size_t)rows * nb * 2, hipMemcpyHostToDevice));
+    CW_HIP(hipMemcpy(w.q + (size_t)row0 * nb * 16, q, (size_t)rows * nb * 16, hipMemcpyHostToDevice));
+    (void)m;
+    return CW_OK;
+}
+
+// Parse "blk.<i>.<name>.weight" -> (layer, tensor id); -1 when not a layer tensor.
+int parse_layer_name(const char *name, int n_layers, int *layer, int *id) {
+    int li = -1, consumed = 0;
+    if (sscanf(name, "blk.%d.%n", &li, &consumed) != 1 || consumed == 0) return -1;
+    if (li < 0 || li >= n_layers) return -2;
+    const char *rest = name + consumed;
+    for (int t = 0; t < T_N; ++t) {
+        std::string want = std::string(kLayerNames[t]) + ".weight";
+        if (want == rest) {
+            *layer = li;
+            *id = t;
+            return 0;
+        }
+    }
+    return -2;
+}
+
+// The shape (out_f, in_f) of a projection.
+void proj_shape(const cw_model *m, int id, int *out_f, int *in_f) {
+    const auto &c = m->cfg;
+    switch (id) {
+        case T_Q: *out_f = m->q_dim; *in_f = c.dim; break;
+        case T_K:
+        case T_V: *out_f = m->kv_dim; *in_f = c.dim; break;
+        case T_O: *out_f = c.dim; *in_f = m->q_dim; break;
+        case T_GATE:
+        case T_UP: *out_f = c.hidden; *in_f = c.dim; break;
+        default: *out_f = c.dim; *in_f = c.hidden; break;  // T_DOWN
+    }
+}
+
+int enqueue_step(cw_model *m) {
+    cw_ctx *ctx = m->ctx;
+    const auto &c = m->cfg;
+    CW_TRY(launch_embed(ctx, m->embed, c.vocab, c.dim, &m->state->token, m->hidden));
+    for (int i = 0; i < c.n_layers; ++i) {
+        Layer &L = m->layers[i];
+        GemvArgs g{};
+        g.x = m->hidden;
+        g.norm_w = L.attn_norm;
+        g.eps = c.eps;
+        g.sA = L.qkv.s;
+        g.qA = L.qkv.q;
+        g.y = m->qkv;
+        g.K = c.dim;
+        g.N = L.qkv.out_f;
+        CW_TRY(launch_q4_gemv(ctx, XS_RMSNORM, EPI_STORE, g));
+
+        AttnArgs a{};
+        a.qkv = m->qkv;
+        a.q_norm_w = L.q_norm;
+        a.k_norm_w = L.k_norm;
+        a.eps = c.eps;
+        a.cos_t = m->cos_t;
+        a.sin_t = m->sin_t;
+        a.k_cache = (char *)m->kcache + (size_t)i * m->kv_layer_bytes;
+        a.v_cache = (char *)m->vcache + (size_t)i * m->kv_layer_bytes;
+        a.kv_dtype = c.kv_dtype;
+        a.n_heads = c.n_heads;
+        a.n_kv = c.n_kv_heads;
+        a.hd = c.head_dim;
+        a.pos_dev = &m->state->pos;
+        a.max_seq = c.max_seq;
+        a.out = m->attn;
+        a.part = m->part;
+        CW_TRY(launch_attention(ctx, a));
+
+        g = GemvArgs{};
+        g.x = m->attn;
+        g.sA = L.wo.s;
+        g.qA = L.wo.q;
+        g.resid = m->hidden;
+        g.y = m->hidden;
+        g.K = m->q_dim;
+        g.N = c.dim;
+        CW_TRY(launch_q4_gemv(ctx, XS_PLAIN, EPI_ADD, g));
+
+        g = GemvArgs{};
+        g.x = m->hidden;
+        g.norm_w = L.ffn_norm;
+        g.eps = c.eps;
+        g.sA = L.gate.s;
+        g.qA = L.gate.q;
+        g.sB = L.up.s;
+        g.qB = L.up.q;
+        g.y = m->act;
+        g.K = c.dim;
+        g.N = c.hidden;
+        CW_TRY(launch_q4_gemv(ctx, XS_RMSNORM, EPI_SWIGLU, g));
+
+        g = GemvArgs{};
+        g.x = m->act;
+        g.sA = L.down.s;
+        g.qA = L.down.q;
+        g.resid = m->hidden;
+        g.y = m->hidden;
+        g.K = c.hidden;
+        g.N = c.dim;
+        CW_TRY(launch_q4_gemv(ctx, XS_PLAIN, EPI_ADD, g));
+    }
+    GemvArgs g{};
+    g.x = m->hidden;
+    g.norm_w = m->final_norm;
+    g.eps = c.eps;
+    g.sA = m->lm_head.s;
+    g.qA = m->lm_head.q;
+    g.y = m->logits;
+    g.K = c.dim;
+    g.N = c.vocab;
+    CW_TRY(launch_q4_gemv(ctx, XS_RMSNORM, EPI_STORE, g));
+    CW_TRY(launch_argmax(ctx, m->logits, c.vocab, m->argmax_out, m->argmax_scratch, m->state,
+                         m->prompt_dev, m->tokens_dev));
+    return CW_OK;
+}
+
+int ensure_graph(cw_model *m) {
+    if (m->graph_exec) return CW_OK;
+    cw_ctx *ctx = m->ctx;
+    const bool prof = ctx->profiling;
+    ctx->profiling = false;
+    CW_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeRelaxed));
+    int rc = enqueue_step(m);
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
+    ctx->profiling = prof;
+    if (rc != CW_OK) {
+        if (graph) hipGraphDestroy(graph);
+        return rc;
+    }
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture", __FILE__, __LINE__);
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        hipGraphDestroy(graph);
+        return hip_fail(e, "hipGraphInstantiate", __FILE__, __LINE__);
+    }
+    m->graph = graph;
+    m->graph_exec = exec;
+    return CW_OK;
+}
+
+int run_steps(cw_model *m, int n, int use_graph) {
+    if (use_graph) {
+        CW_TRY(ensure_graph(m));
+        for (int i = 0; i < n; ++i) CW_HIP(hipGraphLaunch(m->graph_exec, m->ctx->stream));
+    } else {
+        for (int i = 0; i < n; ++i) CW_TRY(enqueue_step(m));
+    }
+    return CW_OK;
+}
+
+int set_state(cw_model *m, const GenState &s) {
+    CW_HIP(hipMemcpyAsync(m->state, &s, sizeof s, hipMemcpyHostToDevice, m->ctx->stream));
+    CW_HIP(hipStreamSynchronize(m->ctx->stream));
+    return CW_OK;
+}
+
+int require_final(cw_model *m, const char *what) {
+    if (!m->finalized) {
+        set_error("%s: model not finalized (call cw_model_finalize)", what);
+        return CW_ERR_STATE;
+    }
+    return CW_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cw_model_create(cw_ctx *ctx, const cw_model_config *cfg, cw_model **out) {
+    CW_CHECK_ARG(ctx && cfg && out, "cw_model_create: null argument");
+    *out = nullptr;
+    const auto &c = *cfg;
+    CW_CHECK_ARG(c.family.norm_unit_gain == 0 && c.family.act == 0 && c.family.qk_norm == 1 &&
+                     c.family.qkv_bias == 0,
+                 "cw_model_create: only the qwen3 family spec is built (plain norm, SwiGLU, "
+                 "qk_norm, no qkv bias)");
+    CW_CHECK_ARG(c.n_layers > 0 && c.dim > 0 && c.n_heads > 0 && c.n_kv_heads > 0 &&
+                     c.hidden > 0 && c.vocab > 0 && c.max_seq > 0,
+                 "cw_model_create: every dimension must be positive");
+    CW_CHECK_ARG(c.n_heads % c.n_kv_heads == 0, "cw_model_create: n_heads %% n_kv_heads != 0");
+    const int hpk = c.n_heads / c.n_kv_heads;
+    CW_CHECK_ARG(hpk == 1 || hpk == 2 || hpk == 4 || hpk == 8,
+                 "cw_model_create: heads per kv head %d not in {1,2,4,8}", hpk);
+    CW_CHECK_ARG(c.head_dim == 16 || c.head_dim == 32 || c.head_dim == 64 || c.head_dim == 128 ||
+                     c.head_dim == 256,
+                 "cw_model_create: head_dim=%d not in {16,32,64,128,256}", c.head_dim);
+    const int q_dim = c.n_heads * c.head_dim, kv_dim = c.n_kv_heads * c.head_dim;
+    CW_CHECK_ARG(c.dim % 32 == 0 && c.hidden % 32 == 0 && q_dim % 32 == 0,
+                 "cw_model_create: dim, hidden and n_heads*head_dim must be multiples of 32");
+    CW_CHECK_ARG(c.dim <= 32768 && c.hidden <= 32768 && q_dim <= 32768,
+                 "cw_model_create: GEMV input width above 32768");
+    CW_CHECK_ARG(c.kv_dtype == CW_F32 || c.kv_dtype == CW_F16, "cw_model_create: kv_dtype=%d",
+                 c.kv_dtype);
+
+    cw_model *m = new cw_model();
+    m->ctx = ctx;
+    m->cfg = c;
+    m->q_dim = q_dim;
+    m->kv_dim = kv_dim;
+    m->layers.resize(c.n_layers);
+    m->have.assign(c.n_layers, std::vector<bool>(T_N, false));
+    auto fail = [&](int rc) {
+        cw_model_destroy(m);
+        return rc;
+    };
+    int rc;
+    for (auto &L : m->layers) {
+        if ((rc = dalloc(m, c.dim * 4, (void **)&L.attn_norm)) ||
+            (rc = dalloc(m, c.head_dim * 4, (void **)&L.q_norm)) ||
+            (rc = dalloc(m, c.head_dim * 4, (void **)&L.k_norm)) ||
+            (rc = dalloc(m, c.dim * 4, (void **)&L.ffn_norm)) ||
+            (rc = alloc_q4(m, L.qkv, q_dim + 2 * kv_dim, c.dim)) ||
+            (rc = alloc_q4(m, L.wo, c.dim, q_dim)) || (rc = alloc_q4(m, L.gate, c.hidden, c.dim)) ||
+            (rc = alloc_q4(m, L.up, c.hidden, c.dim)) || (rc = alloc_q4(m, L.down, c.dim, c.hidden)))
+            return fail(rc);
+    }
+    const size_t es = c.kv_dtype == CW_F16 ? 2 : 4;
+    m->kv_layer_bytes = (size_t)c.max_seq * kv_dim * es;
+    const size_t chunks = ((size_t)c.max_seq + 127) / 128;
+    if ((rc = dalloc(m, (size_t)c.vocab * c.dim * 4, (void **)&m->embed)) ||
+        (rc = dalloc(m, c.dim * 4, (void **)&m->final_norm)) ||
+        (rc = alloc_q4(m, m->lm_head, c.vocab, c.dim)) ||
+        (rc = dalloc(m, m->kv_layer_bytes * c.n_layers, &m->kcache)) ||
+        (rc = dalloc(m, m->kv_layer_bytes * c.n_layers, &m->vcache)) ||
+        (rc = dalloc(m, c.dim * 4, (void **)&m->hidden)) ||
+        (rc = dalloc(m, c.dim * 4, (void **)&m->hidden_out)) ||
+        (rc = dalloc(m, (size_t)(q_dim + 2 * kv_dim) * 4, (void **)&m->qkv)) ||
+        (rc = dalloc(m, (size_t)q_dim * 4, (void **)&m->attn)) ||
+        (rc = dalloc(m, (size_t)c.hidden * 4, (void **)&m->act)) ||
+        (rc = dalloc(m, (size_t)c.vocab * 4, (void **)&m->logits)) ||
+        (rc = dalloc(m, chunks * c.n_heads * (c.head_dim + 2) * 4, (void **)&m->part)) ||
+        (rc = dalloc(m, argmax_scratch_bytes(c.vocab), &m->argmax_scratch)) ||
+        (rc = dalloc(m, sizeof(GenState), (void **)&m->state)) ||
+        (rc = dalloc(m, (size_t)c.max_seq * 4, (void **)&m->prompt_dev)) ||
+        (rc = dalloc(m, (size_t)c.max_seq * 4, (void **)&m->tokens_dev)) ||
+        (rc = dalloc(m, 4, (void **)&m->argmax_out)))
+        return fail(rc);
+    // zero the caches so positions never written read as 0, not garbage
+    if (hipMemset(m->kcache, 0, m->kv_layer_bytes * c.n_layers) != hipSuccess ||
+        hipMemset(m->vcache, 0, m->kv_layer_bytes * c.n_layers) != hipSuccess) {
+        set_error("cw_model_create: hipMemset of the KV cache failed");
+        return fail(CW_ERR_HIP);
+    }
+    const cw_rope_tab *t = nullptr;
+    if ((rc = ctx_rope_table(ctx, c.rope_theta, c.head_dim, c.max_seq, &t))) return fail(rc);
+    m->cos_t = t->cos_t;
+    m->sin_t = t->sin_t;
+    *out = m;
+    return CW_OK;
+}
+
+int cw_model_destroy(cw_model *m) {
+    if (!m) return CW_OK;
+    hipStreamSynchronize(m->ctx->stream);
+    if (m->graph_exec) hipGraphExecDestroy(m->graph_exec);
+    if (m->graph) hipGraphDestroy(m->graph);
+    for (void *p : m->allocs) hipFree(p);
+    delete m;
+    return CW_OK;
+}
+
+int cw_model_set_q4(cw_model *m, const char *name, const uint16_t *scales, const uint8_t *quants) {
+    CW_CHECK_ARG(m && name && scales && quants, "cw_model_set_q4: null argument");
+    if (strcmp(name, "output.weight") == 0) {
+        CW_TRY(upload_rows(m, m->lm_head, 0, m->cfg.vocab, scales, quants));
+        m->have_output = true;
+        return CW_OK;
+    }
+    int li = 0, id = 0;
+    const int pr = parse_layer_name(name, m->cfg.n_layers, &li, &id);
+    CW_CHECK_ARG(pr == 0 && id >= T_Q, "cw_model_set_q4: unknown projection \"%s\"", name);
+    Layer &L = m->layers[li];
+    int out_f = 0, in_f = 0;
+    proj_shape(m, id, &out_f, &in_f);
+    switch (id) {
+        case T_Q: CW_TRY(upload_rows(m, L.qkv, 0, out_f, scales, quants)); break;
+        case T_K: CW_TRY(upload_rows(m, L.qkv, m->q_dim, out_f, scales, quants)); break;
+        case T_V: CW_TRY(upload_rows(m, L.qkv, m->q_dim + m->kv_dim, out_f, scales, quants)); break;
+        case T_O: CW_TRY(upload_rows(m, L.wo, 0, out_f, scales, quants)); break;
+        case T_GATE: CW_TRY(upload_rows(m, L.gate, 0, out_f, scales, quants)); break;
+        case T_UP: CW_TRY(upload_rows(m, L.up, 0, out_f, scales, quants)); break;
+        default: CW_TRY(upload_rows(m, L.down, 0, out_f, scales, quants)); break;
+    }
+    m->have[li][id] = true;
+    return CW_OK;
+}
+
+int cw_model_set_f32(cw_model *m, const char *name, const float *data) {
+    CW_CHECK_ARG(m && name && data, "cw_model_set_f32: null argument");
+    const auto &c = m->cfg;
+    if (strcmp(name, "token_embd.weight") == 0) {
+        CW_HIP(hipMemcpy(m->embed, data, (size_t)c.vocab * c.dim * 4, hipMemcpyHostToDevice));
+        m->have_embed = true;
+        return CW_OK;
+    }
+    if (strcmp(name, "output_norm.weight") == 0) {
+        CW_HIP(hipMemcpy(m->final_norm, data, (size_t)c.dim * 4, hipMemcpyHostToDevice));
+        m->have_final = true;
+        return CW_OK;
+    }
+    int li = 0, id = 0;
+    const int pr = parse_layer_name(name, c.n_layers, &li, &id);
+    CW_CHECK_ARG(pr == 0 && id < T_Q, "cw_model_set_f32: unknown vector \"%s\"", name);
+    Layer &L = m->layers[li];
+    float *dst = id == T_ATTN_NORM ? L.attn_norm
+                 : id == T_Q_NORM  ? L.q_norm
+                 : id == T_K_NORM  ? L.k_norm
+                                   : L.ffn_norm;
+    const size_t n = (id == T_Q_NORM || id == T_K_NORM) ? c.head_dim : c.dim;
+    CW_HIP(hipMemcpy(dst, data, n * 4, hipMemcpyHostToDevice));
+    m->have[li][id] = true;
+    return CW_OK;
+}
+
+int cw_model_load_synthetic(cw_model *m, uint64_t seed) {
+    CW_CHECK_ARG(m != nullptr, "cw_model_load_synthetic: null model");
+    const auto &c = m->cfg;
+    std::vector<uint16_t> s;
+    std::vector<uint8_t> q;
+    std::vector<float> f;
+    char name[96];
+    for (int i = 0; i < c.n_layers; ++i) {
+        for (int id = 0; id < T_N; ++id) {
+            snprintf(name, sizeof name, "blk.%d.%s.weight", i, kLayerNames[id]);
+            const uint64_t key = cw_synth_key(seed, name);
+            if (id < T_Q) {
+                const size_t n = (id == T_Q_NORM || id == T_K_NORM) ? c.head_dim : c.dim;
+                f.resize(n);
+                CW_TRY(cw_synth_normal_f32(key, n, 1.0f, 0.02f, f.data()));
+                CW_TRY(cw_model_set_f32(m, name, f.data()));
+            } else {
+                int out_f = 0, in_f = 0;
+                proj_shape(m, id, &out_f, &in_f);
+                const size_t nblk = (size_t)out_f * (in_f / 32);
+                s.resize(nblk);
+                q.resize(nblk * 16);
+                CW_TRY(cw_synth_q4(key, nblk, 0.02f, s.data(), q.data()));
+                CW_TRY(cw_model_set_q4(m, name, s.data(), q.data()));
+            }
+        }
+    }
+    f.resize(c.dim);
+    CW_TRY(cw_synth_normal_f32(cw_synth_key(seed, "output_norm.weight"), c.dim, 1.0f, 0.02f,
+                               f.data()));
+    CW_TRY(cw_model_set_f32(m, "output_norm.weight", f.data()));
+    f.resize((size_t)c.vocab * c.dim);
+    CW_TRY(cw_synth_normal_f32(cw_synth_key(seed, "token_embd.weight"), f.size(), 0.0f, 0.02f,
+                               f.data()));
+    CW_TRY(cw_model_set_f32(m, "token_embd.weight", f.data()));
+    return CW_OK;
+}
+
+int cw_model_finalize(cw_model *m) {
+    CW_CHECK_ARG(m != nullptr, "cw_model_finalize: null model");
+    const auto &c = m->cfg;
+    for (int i = 0; i < c.n_layers; ++i)
+        for (int id = 0; id < T_N; ++id)
+            if (!m->have[i][id]) {
+                set_error("missing tensor blk.%d.%s.weight", i, kLayerNames[id]);
+                return CW_ERR_STATE;
+            }
+    if (!m->have_embed) {
+        set_error("missing tensor token_embd.weight");
+        return CW_ERR_STATE;
+    }
+    if (!m->have_final) {
+        set_error("missing tensor output_norm.weight");
+        return CW_ERR_STATE;
+    }
+    if (!m->have_output) {
+        // tied LM head (qwen3.rs:93-98): re-quantize the f32 embedding
+        std::vector<float> e((size_t)c.vocab * c.dim);
+        CW_HIP(hipMemcpy(e.data(), m->embed, e.size() * 4, hipMemcpyDeviceToHost));
+        const size_t nblk = (size_t)c.vocab * (c.dim / 32);
+        std::vector<uint16_t> s(nblk);
+        std::vector<uint8_t> q(nblk * 16);
+        CW_TRY(cw_q4_quantize(e.data(), c.vocab, c.dim, s.data(), q.data()));
+        CW_TRY(upload_rows(m, m->lm_head, 0, c.vocab, s.data(), q.data()));
+    }
+    m->finalized = true;
+    return CW_OK;
+}
+
+int cw_model_prefill_kv(cw_model *m, const void *k, const void *v, int n_pos) {
+    CW_CHECK_ARG(m && k && v, "cw_model_prefill_kv: null argument");
+    CW_CHECK_ARG(n_pos > 0 && n_pos <= m->cfg.max_seq, "cw_model_prefill_kv: n_pos=%d (max_seq %d)",
+                 n_pos, m->cfg.max_seq);
+    const size_t es = m->cfg.kv_dtype == CW_F16 ? 2 : 4;
+    const size_t row = (size_t)n_pos * m->kv_dim * es;
+    for (int l = 0; l < m->cfg.n_layers; ++l) {
+        CW_HIP(hipMemcpy((char *)m->kcache + l * m->kv_layer_bytes, (const char *)k + l * row, row,
+                         hipMemcpyHostToDevice));
+        CW_HIP(hipMemcpy((char *)m->vcache + l * m->kv_layer_bytes, (const char *)v + l * row, row,
+                         hipMemcpyHostToDevice));
+    }
+    return CW_OK;
+}
+
+int cw_model_step(cw_model *m, uint32_t token, int pos, uint32_t *argmax_out) {
+    CW_CHECK_ARG(m != nullptr, "cw_model_step: null model");
+    CW_TRY(require_final(m, "cw_model_step"));
+    CW_CHECK_ARG(token < (uint32_t)m->cfg.vocab, "cw_model_step: token %u >= vocab %d", token,
+                 m->cfg.vocab);
+    CW_CHECK_ARG(pos >= 0 && pos < m->cfg.max_seq, "cw_model_step: pos=%d outside [0, %d)", pos,
+                 m->cfg.max_seq);
+    GenState s{pos, token, pos, 0, 0, 0};
+    CW_TRY(set_state(m, s));
+    CW_TRY(enqueue_step(m));
+    CW_TRY(launch_rmsnorm(m->ctx, m->hidden, m->final_norm, 1, m->cfg.dim, m->cfg.eps,
+                          m->hidden_out));
+    uint32_t r = 0;
+    CW_HIP(hipMemcpyAsync(&r, m->argmax_out, 4, hipMemcpyDeviceToHost, m->ctx->stream));
+    CW_HIP(hipStreamSynchronize(m->ctx->stream));
+    if (argmax_out) *argmax_out = r;
+    return CW_OK;
+}
+
+int cw_model_logits(cw_model *m, float *host_out) {
+    CW_CHECK_ARG(m && host_out, "cw_model_logits: null argument");
+    return cw_download(m->ctx, host_out, m->logits, (size_t)m->cfg.vocab * 4);
+}
+
+int cw_model_hidden(cw_model *m, float *host_out) {
+    CW_CHECK_ARG(m && host_out, "cw_model_hidden: null argument");
+    return cw_download(m->ctx, host_out, m->hidden_out, (size_t)m->cfg.dim * 4);
+}
+
+int cw_generate(cw_model *m, const uint32_t *prompt, int n_prompt, int max_new, int start_pos,
+                int use_graph, uint32_t *out_tokens) {
+    CW_CHECK_ARG(m && prompt && out_tokens, "cw_generate: null argument");
+    CW_TRY(require_final(m, "cw_generate"));
+    CW_CHECK_ARG(n_prompt >= 1 && max_new >= 1, "cw_generate: n_prompt=%d max_new=%d", n_prompt,
+                 max_new);
+    const long total = (long)n_prompt + max_new - 1;
+    CW_CHECK_ARG(start_pos >= 0 && start_pos + total <= m->cfg.max_seq,
+                 "cw_generate: positions [%d, %ld) exceed max_seq %d", start_pos,
+                 start_pos + total, m->cfg.max_seq);
+    for (int i = 0; i < n_prompt; ++i)
+        CW_CHECK_ARG(prompt[i] < (uint32_t)m->cfg.vocab, "cw_generate: prompt[%d]=%u >= vocab", i,
+                     prompt[i]);
+    CW_HIP(hipMemcpy(m->prompt_dev, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice));
+    GenState s{start_pos, prompt[0], start_pos, n_prompt, 0, max_new};
+    CW_TRY(set_state(m, s));
+    CW_TRY(run_steps(m, (int)total, use_graph));
+    CW_HIP(hipMemcpyAsync(out_tokens, m->tokens_dev, (size_t)max_new * 4, hipMemcpyDeviceToHost,
+                          m->ctx->stream));
+    CW_HIP(hipStreamSynchronize(m->ctx->stream));
+    return CW_OK;
+}
+
+int cw_model_reset_state(cw_model *m, uint32_t token, int pos) {
+    CW_CHECK_ARG(m != nullptr, "cw_model_reset_state: null model");
+    CW_CHECK_ARG(token < (uint32_t)m->cfg.vocab && pos >= 0 && pos < m->cfg.max_seq,
+                 "cw_model_reset_state: token=%u pos=%d", token, pos);
+    GenState s{pos, token, pos, 1, 0, m->cfg.max_seq};
+    return set_state(m, s);
+}
+
+int cw_model_decode_async(cw_model *m, int n_steps, int use_graph) {
+    CW_CHECK_ARG(m != nullptr && n_steps >= 0, "cw_model_decode_async: bad argument");
+    CW_TRY(require_final(m, "cw_model_decode_async"));
+    GenState s{};
+    CW_HIP(hipMemcpyAsync(&s, m->state, sizeof s, hipMemcpyDeviceToHost, m->ctx->stream));
+    CW_HIP(hipStreamSynchronize(m->ctx->stream));
+    CW_CHECK_ARG(s.pos + n_steps <= m->cfg.max_seq,
+                 "cw_model_decode_async: %d steps from pos %d exceed max_seq %d", n_steps, s.pos,
+                 m->cfg.max_seq);
+    return run_steps(m, n_steps, use_graph);
+}
+
+int cw_model_tokens(cw_model *m, uint32_t *host_out, int max_n, int *n_out) {
+    CW_CHECK_ARG(m && host_out && n_out, "cw_model_tokens: null argument");
+    GenState s{};
+    CW_HIP(hipMemcpyAsync(&s, m->state, sizeof s, hipMemcpyDeviceToHost, m->ctx->stream));
+    CW_HIP(hipStreamSynchronize(m->ctx->stream));
+    int n = s.produced < s.max_out ? s.produced : s.max_out;
+    if (n > max_n) n = max_n;
+    if (n > 0) CW_TRY(cw_download(m->ctx, host_out, m->tokens_dev, (size_t)n * 4));
+    *n_out = n;
+    return CW_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,403 @@
+// Q4_0 dequant-fused GEMV for gfx950 (decode, one token).
+//
+// Replaces q4::gemv (src/kernels/q4.rs:9-30) and its shader q4.wgsl:25-82.
+// Same arithmetic identity as the shader, y[o] = sum_b d[o,b] *
+// (sum_j q_j x_j - 8 * sum_j x_j), over GGUF Q4_0 blocks kept packed in HBM.
+//
+// Layout in HBM (split GGUF Q4_0): quants [N][K/32][16] bytes (one 128-bit
+// load per block), scales [N][K/32] f16.  Byte j of a block holds element j
+// in its low nibble and element j+16 in its high nibble.
+//
+// Work split: a wave64 covers 64 blocks per step.  G = lanes per row (the
+// largest power of two <= 64 dividing K/32); 64/G rows share a wave step.
+// Each wave owns R row slots at a time; waves walk a persistent grid of
+// wave tiles.  The activation is staged once per workgroup into LDS as
+// [8][K/32] float4 (conflict-free: lane b reads float4 i of block b) plus the
+// per-block sums sum_j x_j.
+//
+// Nibble decode costs 5 VALU ops per 8 weights: AND-ing a quant dword with
+// 0x000F000F / 0x00F000F0 (and the same after one >>8) leaves two f16
+// *subnormals* whose values are q*2^-24 and q*2^-20 exactly.  v_fma_mix_f32
+// widens either f16 half to f32 inside the FMA, so with the LDS copy of x
+// pre-scaled by 2^24 (elements 0..15 of a block) and 2^20 (elements 16..31)
+// each weight costs one fma_mix: q*x accumulated in f32 with no rounding
+// beyond the reference's own multiply-add.  8 fma_mix + 5 bit ops per 8
+// weights keeps the VALU below the HBM rate on 256 CUs.
+//
+// Optional prologue: RMSNorm of the raw hidden state (norm.wgsl:20-42) while
+// staging.  Optional epilogues: residual add (ewise.wgsl:9-13) and SwiGLU of
+// a gate/up row pair (glu.wgsl:22-26).
+
+#include <map>
+#include <mutex>
+
+#include "cw_internal.hpp"
+
+namespace {
+
+using cwi::GemvArgs;
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// All-reduce sum within aligned groups of G lanes (G a power of two <= 64).
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (G >= 2) v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+    if constexpr (G >= 4) v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+    if constexpr (G >= 8) v += dpp<0x141>(v);  // row_half_mirror
+    if constexpr (G >= 16) v += dpp<0x140>(v); // row_mirror
+    if constexpr (G >= 32) v += __shfl_xor(v, 16);
+    if constexpr (G >= 64) v += __shfl_xor(v, 32);
+    return v;
+}
+
+__device__ __forceinline__ float f16lo(uint32_t v) {
+    return (float)__builtin_bit_cast(half2v, v).x;
+}
+__device__ __forceinline__ float f16hi(uint32_t v) {
+    return (float)__builtin_bit_cast(half2v, v).y;
+}
+
+// sum_j q_j * x_j over one block; xl[w] = 2^24 * x[4w..4w+3],
+// xh[w] = 2^20 * x[16+4w..16+4w+3].
+__device__ __forceinline__ float dot_word(uint32_t dw, float4 xl, float4 xh, float s) {
+    const uint32_t a = dw & 0x000F000Fu;          // elements 4w+0, 4w+2     (q * 2^-24)
+    const uint32_t b = dw & 0x00F000F0u;          // elements 16+4w+0, +2    (q * 2^-20)
+    const uint32_t d8 = dw >> 8;
+    const uint32_t c = d8 & 0x000F000Fu;          // elements 4w+1, 4w+3
+    const uint32_t e = d8 & 0x00F000F0u;          // elements 16+4w+1, +3
+    s = __builtin_fmaf(f16lo(a), xl.x, s);
+    s = __builtin_fmaf(f16lo(c), xl.y, s);
+    s = __builtin_fmaf(f16hi(a), xl.z, s);
+    s = __builtin_fmaf(f16hi(c), xl.w, s);
+    s = __builtin_fmaf(f16lo(b), xh.x, s);
+    s = __builtin_fmaf(f16lo(e), xh.y, s);
+    s = __builtin_fmaf(f16hi(b), xh.z, s);
+    s = __builtin_fmaf(f16hi(e), xh.w, s);
+    return s;
+}
+
+template <int G, int R, int XS, int EPI>
+__global__ __launch_bounds__(kThreads) void q4_gemv_kernel(GemvArgs a, int n_wave_tiles) {
+    extern __shared__ float4 lds4[];
+    __shared__ float red[kWaves];
+    const int K = a.K;
+    const int nb = K >> 5;
+    const int K4 = K >> 2;
+    float *sx = reinterpret_cast<float *>(lds4 + 8 * nb);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+
+    // ---- stage the activation (optionally RMS-normalised) ----
+    float inv = 1.0f;
+    if constexpr (XS == cwi::XS_RMSNORM) {
+        float ss = 0.0f;
+        for (int i = tid; i < K4; i += kThreads) {
+            float4 v = reinterpret_cast<const float4 *>(a.x)[i];
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+        ss = group_sum<64>(ss);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        ss = (red[0] + red[1]) + (red[2] + red[3]);
+        inv = 1.0f / sqrtf(ss / (float)K + a.eps);
+    }
+    for (int idx = tid; idx < K4; idx += kThreads) {
+        float4 v = reinterpret_cast<const float4 *>(a.x)[idx];
+        if constexpr (XS == cwi::XS_RMSNORM) {
+            float4 w = reinterpret_cast<const float4 *>(a.norm_w)[idx];
+            v.x = (v.x * inv) * w.x;
+            v.y = (v.y * inv) * w.y;
+            v.z = (v.z * inv) * w.z;
+            v.w = (v.w * inv) * w.w;
+        }
+        const int blk = idx >> 3, i = idx & 7;
+        const float sc = i < 4 ? 0x1p24f : 0x1p20f;
+        lds4[i * nb + blk] = make_float4(v.x * sc, v.y * sc, v.z * sc, v.w * sc);
+        // the 8 float4 of a block sit in 8 consecutive lanes
+        float part = (v.x + v.y) + (v.z + v.w);
+        part = group_sum<8>(part);
+        if (i == 0) sx[blk] = part;
+    }
+    __syncthreads();
+
+    // ---- stream the weights ----
+    constexpr int RPS = 64 / G;  // rows per wave step
+    constexpr int NR = (EPI == cwi::EPI_SWIGLU) ? R / 2 : R;  // distinct rows per slot group
+    constexpr int ROWS_PER_TILE = NR * RPS;
+    const int s = lane & (G - 1);
+    const int rl = lane / G;
+    const int N = a.N;
+
+    for (int wt = blockIdx.x * kWaves + wave; wt < n_wave_tiles; wt += gridDim.x * kWaves) {
+        const int row0 = wt * ROWS_PER_TILE;
+        const uint4 *qp[R];
+        const uint16_t *sp[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int rr = r % NR;
+            int row = row0 + rr * RPS + rl;
+            row = row < N ? row : N - 1;
+            const bool second = (EPI == cwi::EPI_SWIGLU) && r >= NR;
+            const uint8_t *qb = second ? a.qB : a.qA;
+            const uint16_t *sb = second ? a.sB : a.sA;
+            qp[r] = reinterpret_cast<const uint4 *>(qb) + (size_t)row * nb;
+            sp[r] = sb + (size_t)row * nb;
+        }
+        float acc[R];
+        uint4 qv[R];
+        uint32_t dv[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            acc[r] = 0.0f;
+            qv[r] = qp[r][s];
+            dv[r] = sp[r][s];
+        }
+        for (int b = s; b < nb; b += G) {
+            uint4 qn[R];
+            uint32_t dn[R];
+            const int bn = b + G;
+            if (bn < nb) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    qn[r] = qp[r][bn];
+                    dn[r] = sp[r][bn];
+                }
+            }
+            float4 xv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xv[i] = lds4[i * nb + b];
+            const float sxb = sx[b];
+            float sum[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) sum[r] = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const uint32_t dw = w == 0 ? qv[r].x : w == 1 ? qv[r].y : w == 2 ? qv[r].z : qv[r].w;
+                    sum[r] = dot_word(dw, xv[w], xv[4 + w], sum[r]);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float t = __builtin_fmaf(-8.0f, sxb, sum[r]);
+                const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)dv[r]);
+                acc[r] = __builtin_fmaf((float)d, t, acc[r]);
+            }
+            if (bn < nb) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    qv[r] = qn[r];
+                    dv[r] = dn[r];
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = group_sum<G>(acc[r]);
+        if (s == 0) {
+#pragma unroll
+            for (int rr = 0; rr < NR; ++rr) {
+                const int row = row0 + rr * RPS + rl;
+                if (row < N) {
+                    if constexpr (EPI == cwi::EPI_STORE) {
+                        a.y[row] = acc[rr];
+                    } else if constexpr (EPI == cwi::EPI_ADD) {
+                        a.y[row] = a.resid[row] + acc[rr];
+                    } else {
+                        const float g = acc[rr], u = acc[rr + NR];
+                        const float sg = g / (1.0f + expf(-g));
+                        a.y[row] = sg * u;
+                    }
+                }
+            }
+        }
+    }
+}
+
+typedef void (*gemv_fn)(GemvArgs, int);
+
+template <int G, int R, int XS>
+gemv_fn pick_epi(int epi) {
+    switch (epi) {
+        case cwi::EPI_STORE: return q4_gemv_kernel<G, R, XS, cwi::EPI_STORE>;
+        case cwi::EPI_ADD: return q4_gemv_kernel<G, R, XS, cwi::EPI_ADD>;
+        default: return q4_gemv_kernel<G, R, XS, cwi::EPI_SWIGLU>;
+    }
+}
+
+template <int G, int R>
+gemv_fn pick_xs(int xs, int epi) {
+    return xs == cwi::XS_RMSNORM ? pick_epi<G, R, cwi::XS_RMSNORM>(epi)
+                                 : pick_epi<G, R, cwi::XS_PLAIN>(epi);
+}
+
+template <int G>
+gemv_fn pick_r(int r, int xs, int epi) {
+    return r == 4 ? pick_xs<G, 4>(xs, epi) : pick_xs<G, 2>(xs, epi);
+}
+
+gemv_fn pick(int g, int r, int xs, int epi) {
+    switch (g) {
+        case 64: return pick_r<64>(r, xs, epi);
+        case 32: return pick_r<32>(r, xs, epi);
+        case 16: return pick_r<16>(r, xs, epi);
+        case 8: return pick_r<8>(r, xs, epi);
+        case 4: return pick_r<4>(r, xs, epi);
+        case 2: return pick_r<2>(r, xs, epi);
+        default: return pick_r<1>(r, xs, epi);
+    }
+}
+
+struct OccKey {
+    const void *fn;
+    int lds;
+    bool operator<(const OccKey &o) const { return fn != o.fn ? fn < o.fn : lds < o.lds; }
+};
+
+std::mutex g_occ_mu;
+std::map<OccKey, int> g_occ;
+std::map<const void *, bool> g_attr_set;
+
+int occupancy(gemv_fn fn, int lds, int *blocks) {
+    std::lock_guard<std::mutex> lk(g_occ_mu);
+    const void *f = reinterpret_cast<const void *>(fn);
+    if (!g_attr_set[f]) {
+        CW_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+        g_attr_set[f] = true;
+    }
+    OccKey k{f, lds};
+    auto it = g_occ.find(k);
+    if (it != g_occ.end()) {
+        *blocks = it->second;
+        return CW_OK;
+    }
+    int nb = 0;
+    CW_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, kThreads, (size_t)lds));
+    if (nb < 1) nb = 1;
+    g_occ[k] = nb;
+    *blocks = nb;
+    return CW_OK;
+}
+
+const char *label_of(int xs, int epi) {
+    static const char *names[2][3] = {
+        {"q4_gemv", "q4_gemv_add", "q4_gemv_swiglu"},
+        {"q4_gemv_rmsnorm", "q4_gemv_rmsnorm_add", "q4_gemv_rmsnorm_swiglu"}};
+    return names[xs][epi];
+}
+
+}  // namespace
+
+namespace cwi {
+
+int launch_q4_gemv(cw_ctx *ctx, XSrc xs, Epi epi, const GemvArgs &a) {
+    const int nb = a.K / 32;
+    int g = 64;
+    while (g > 1 && nb % g) g >>= 1;
+    const int rps = 64 / g;
+    auto tiles_for = [&](int r) {
+        const int nr = epi == EPI_SWIGLU ? r / 2 : r;
+        const int rows = nr * rps;
+        return (a.N + rows - 1) / rows;
+    };
+    int r = 4;
+    if ((tiles_for(4) + kWaves - 1) / kWaves < 2 * ctx->n_cu) r = 2;
+    const int n_tiles = tiles_for(r);
+    gemv_fn fn = pick(g, r, xs, epi);
+    const int lds = nb * 132;
+    int occ = 1;
+    CW_TRY(occupancy(fn, lds, &occ));
+    int grid = (n_tiles + kWaves - 1) / kWaves;
+    const int resident = ctx->n_cu * occ;
+    if (grid > resident) grid = resident;
+    prof_begin(ctx, label_of(xs, epi));
+    hipLaunchKernelGGL(fn, dim3(grid), dim3(kThreads), lds, ctx->stream, a, n_tiles);
+    prof_end(ctx);
+    return launch_check(label_of(xs, epi));
+}
+
+}  // namespace cwi
+
+using namespace cwi;
+
+static int check_q4_shape(const char *what, int in_f, int out_f) {
+    CW_CHECK_ARG(in_f > 0 && in_f % 32 == 0, "%s: in_f=%d must be a positive multiple of 32", what,
+                 in_f);
+    CW_CHECK_ARG(in_f <= 32768, "%s: in_f=%d exceeds 32768", what, in_f);
+    CW_CHECK_ARG(out_f > 0, "%s: out_f=%d must be positive", what, out_f);
+    return CW_OK;
+}
+
+// x and quants are read with 128-bit loads, scales with 16-bit loads.
+static int check_q4_align(const char *what, const float *x, const uint16_t *s, const uint8_t *q) {
+    CW_CHECK_ARG(((uintptr_t)x & 15) == 0, "%s: x must be 16-byte aligned", what);
+    CW_CHECK_ARG(((uintptr_t)q & 15) == 0, "%s: quants must be 16-byte aligned", what);
+    CW_CHECK_ARG(((uintptr_t)s & 1) == 0, "%s: scales must be 2-byte aligned", what);
+    return CW_OK;
+}
+
+extern "C" {
+
+int cw_q4_gemv(cw_ctx *ctx, const float *x, const uint16_t *scales, const uint8_t *quants,
+               int in_f, int out_f, float *y) {
+    CW_CHECK_ARG(ctx && x && scales && quants && y, "cw_q4_gemv: null argument");
+    CW_TRY(check_q4_shape("cw_q4_gemv", in_f, out_f));
+    CW_TRY(check_q4_align("cw_q4_gemv", x, scales, quants));
+    GemvArgs a{};
+    a.x = x;
+    a.sA = scales;
+    a.qA = quants;
+    a.y = y;
+    a.K = in_f;
+    a.N = out_f;
+    return launch_q4_gemv(ctx, XS_PLAIN, EPI_STORE, a);
+}
+
+int cw_q4_gemv_add(cw_ctx *ctx, const float *x, const uint16_t *scales, const uint8_t *quants,
+                   int in_f, int out_f, const float *residual, float *y) {
+    CW_CHECK_ARG(ctx && x && scales && quants && residual && y, "cw_q4_gemv_add: null argument");
+    CW_TRY(check_q4_shape("cw_q4_gemv_add", in_f, out_f));
+    CW_TRY(check_q4_align("cw_q4_gemv_add", x, scales, quants));
+    GemvArgs a{};
+    a.x = x;
+    a.sA = scales;
+    a.qA = quants;
+    a.resid = residual;
+    a.y = y;
+    a.K = in_f;
+    a.N = out_f;
+    return launch_q4_gemv(ctx, XS_PLAIN, EPI_ADD, a);
+}
+
+int cw_q4_gemv_swiglu(cw_ctx *ctx, const float *x, const uint16_t *gate_scales,
+                      const uint8_t *gate_quants, const uint16_t *up_scales,
+                      const uint8_t *up_quants, int in_f, int out_f, float *y) {
+    CW_CHECK_ARG(ctx && x && gate_scales && gate_quants && up_scales && up_quants && y,
+                 "cw_q4_gemv_swiglu: null argument");
+    CW_TRY(check_q4_shape("cw_q4_gemv_swiglu", in_f, out_f));
+    CW_TRY(check_q4_align("cw_q4_gemv_swiglu", x, gate_scales, gate_quants));
+    CW_TRY(check_q4_align("cw_q4_gemv_swiglu", x, up_scales, up_quants));
+    GemvArgs a{};
+    a.x = x;
+    a.sA = gate_scales;
+    a.qA = gate_quants;
+    a.sB = up_scales;
+    a.qB = up_quants;
+    a.y = y;
+    a.K = in_f;
+    a.N = out_f;
+    return launch_q4_gemv(ctx, XS_PLAIN, EPI_SWIGLU, a);
+}
+
+}  // extern "C"

@@ -1,0 +1,230 @@
+/*
+ * chat_wgpu.h -- C ABI of the MI355X-native chat-wgpu decode path.
+ *
+ * Plain C: opaque handles, raw pointers and sizes, int status codes.  Device
+ * pointers are HIP device addresses (from cw_alloc / cw_frame_alloc); host
+ * pointers are ordinary memory.  Every entry point returns CW_OK (0) or a
+ * negative CW_ERR_*; cw_last_error() then holds a message (thread-local).
+ * Kernel entry points validate their arguments on the host before anything
+ * is launched and enqueue asynchronously on the context's single HIP stream;
+ * only cw_download, cw_flush, cw_profile_report and the cw_model_* calls that
+ * return host data synchronise.  A context is not thread-safe (the reference's
+ * GpuContext is !Sync, src/context.rs:9,29-56).
+ *
+ * Each declaration names the reference interface it replaces (file:line in
+ * EggerMarc/chat-wgpu).
+ */
+#ifndef CHAT_WGPU_H
+#define CHAT_WGPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CW_OK 0
+#define CW_ERR_ARG (-1)     /* invalid argument (shape, null pointer, range) */
+#define CW_ERR_HIP (-2)     /* a HIP runtime call failed */
+#define CW_ERR_OOM (-3)     /* device or host allocation failed */
+#define CW_ERR_STATE (-4)   /* call not valid in the current state */
+
+/* element types of a KV cache */
+#define CW_F32 0
+#define CW_F16 1
+
+typedef struct cw_ctx cw_ctx;
+typedef struct cw_model cw_model;
+
+/* ---------------------------------------------------------------- */
+/* Context: device, stream, arena (src/context.rs)                   */
+/* ---------------------------------------------------------------- */
+
+/* GpuContext::new (src/context.rs:60-104): open `device`, create the stream. */
+int cw_ctx_create(int device, cw_ctx **out);
+/* Drop for GpuContext: waits for the stream, frees every allocation. */
+int cw_ctx_destroy(cw_ctx *ctx);
+/* Text of the last error on this thread ("" if none). */
+const char *cw_last_error(void);
+/* Library version string. */
+const char *cw_version(void);
+/* Device facts: compute units, HBM bytes, gfx arch name. */
+int cw_device_info(cw_ctx *ctx, int *n_cu, size_t *hbm_bytes, char *arch, size_t arch_len);
+
+/* GpuContext::empty_persistent / storage (src/context.rs:177-227): a
+ * persistent device allocation, 256-byte aligned. */
+int cw_alloc(cw_ctx *ctx, size_t bytes, void **out);
+int cw_free(cw_ctx *ctx, void *ptr);
+/* GpuContext::empty (src/context.rs:210-227): per-frame scratch.  Valid until
+ * cw_frame_reset; the same call sequence after a reset returns the same
+ * addresses (the arena is deterministic, like the reference's). */
+int cw_frame_alloc(cw_ctx *ctx, size_t bytes, void **out);
+/* GpuContext::reset_frame (src/context.rs:237-240). */
+int cw_frame_reset(cw_ctx *ctx);
+/* GpuContext::storage's upload (create_buffer_init, src/context.rs:177-194):
+ * host -> device, ordered on the stream. */
+int cw_upload(cw_ctx *ctx, void *dst_dev, const void *src_host, size_t bytes);
+/* GpuContext::read (src/context.rs:361-389): flush, then device -> host;
+ * returns after the data is on the host. */
+int cw_download(cw_ctx *ctx, void *dst_host, const void *src_dev, size_t bytes);
+/* GpuContext::copy (src/context.rs:255-269): device -> device on the stream. */
+int cw_copy(cw_ctx *ctx, void *dst_dev, const void *src_dev, size_t bytes);
+/* GpuContext::flush (src/context.rs:141-151): wait until the stream drains. */
+int cw_flush(cw_ctx *ctx);
+
+/* ---------------------------------------------------------------- */
+/* Kernels (src/kernels/NAME.rs).  Q4 weights are GGUF Q4_0 split into   */
+/* two arrays: scales = f16 bits [out_f][in_f/32], quants = the 16     */
+/* packed bytes of every block [out_f][in_f/32][16] (low nibble of byte */
+/* j -> element j, high nibble -> element j+16; value d*(q-8)).        */
+/* ---------------------------------------------------------------- */
+
+/* q4::gemv (src/kernels/q4.rs:9-30, q4.wgsl:25-82): y[out_f] = W x[in_f].
+ * in_f must be a positive multiple of 32 and at most 32768. */
+int cw_q4_gemv(cw_ctx *ctx, const float *x, const uint16_t *scales, const uint8_t *quants,
+               int in_f, int out_f, float *y);
+/* q4::gemv followed by attention::add (src/model/qwen3.rs:178-179,186-187):
+ * y = residual + W x.  y may alias residual. */
+int cw_q4_gemv_add(cw_ctx *ctx, const float *x, const uint16_t *scales, const uint8_t *quants,
+                   int in_f, int out_f, const float *residual, float *y);
+/* gate/up q4::gemv then activation::swiglu (src/model/qwen3.rs:183-185):
+ * y = silu(Wg x) * (Wu x), both matrices [out_f][in_f]. */
+int cw_q4_gemv_swiglu(cw_ctx *ctx, const float *x, const uint16_t *gate_scales,
+                      const uint8_t *gate_quants, const uint16_t *up_scales,
+                      const uint8_t *up_quants, int in_f, int out_f, float *y);
+/* norm::rmsnorm (src/kernels/norm.rs:26-29, norm.wgsl:20-42): per row
+ * y = x * inverseSqrt(sum(x^2)/dim + eps) * w. */
+int cw_rmsnorm(cw_ctx *ctx, const float *x, const float *w, int rows, int dim, float eps, float *y);
+/* rope::rope (src/kernels/rope.rs:8-27, rope.wgsl:18-35): NeoX rotate-half of
+ * rows x head_dim at position pos.  Angles pos*theta^(-2i/hd) come from a
+ * table evaluated in f64 and rounded to f32. */
+int cw_rope(cw_ctx *ctx, const float *x, int rows, int head_dim, int pos, float theta, float *y);
+/* attention::attention (src/kernels/attention.rs:7-38, attention.wgsl:23-96):
+ * single-query GQA attention over seq positions of a [seq][n_kv*hd] cache of
+ * element type kv_dtype (CW_F32 or CW_F16).  head_dim in {16,32,64,128,256}. */
+int cw_attention(cw_ctx *ctx, const float *q, const void *k, const void *v, int kv_dtype,
+                 int n_heads, int n_kv_heads, int seq, int head_dim, float *out);
+/* attention::add (src/kernels/attention.rs:40-51, ewise.wgsl:9-13): c = a + b. */
+int cw_add(cw_ctx *ctx, const float *a, const float *b, int n, float *c);
+/* activation::swiglu (src/kernels/activation.rs:42-44, glu.wgsl:22-26). */
+int cw_swiglu(cw_ctx *ctx, const float *gate, const float *up, int n, float *out);
+/* argmax::argmax (src/kernels/argmax.rs:11-18, argmax.wgsl:18-55): index of
+ * the maximum, lowest index among equals, written to out_dev[0]. */
+int cw_argmax(cw_ctx *ctx, const float *logits, int n, uint32_t *out_dev);
+/* KvCache::write (src/model/cache.rs:21-24): k,v [kv_dim] f32 -> row pos of
+ * the caches (converted to f16, round to nearest even, for CW_F16). */
+int cw_kv_write(cw_ctx *ctx, void *k_cache, void *v_cache, int kv_dtype, int pos, int kv_dim,
+                const float *k, const float *v);
+/* Qwen3::embed (src/model/qwen3.rs:128-133) plus clone_buf (qwen3.rs:194-197):
+ * out = table[token_dev[0]] + 0, token read on the device (< vocab). */
+int cw_embed(cw_ctx *ctx, const float *table, int vocab, int dim, const uint32_t *token_dev,
+             float *out);
+
+/* ---------------------------------------------------------------- */
+/* Host-side Q4 helpers                                              */
+/* ---------------------------------------------------------------- */
+
+/* q4::quantize_q4_0 (src/kernels/q4.rs:37-61) producing GGUF Q4_0: d =
+ * absmax/8 rounded to f16, q = clamp(round(v/d)+8, 0, 15) against the stored
+ * f16 d.  data is [out_f][in_f] row-major; in_f % 32 == 0. */
+int cw_q4_quantize(const float *data, size_t out_f, size_t in_f, uint16_t *scales,
+                   uint8_t *quants);
+/* GGUF Q4_0 18-byte blocks (dequant.rs:60-78 layout) -> split image. */
+int cw_q4_split_blocks(const uint8_t *blocks, size_t nblocks, uint16_t *scales, uint8_t *quants);
+
+/* ---------------------------------------------------------------- */
+/* Seeded synthetic data (counter-based, independent of thread count) */
+/* ---------------------------------------------------------------- */
+
+/* Stream key of a named tensor: FNV-1a 64 of the name mixed with seed. */
+uint64_t cw_synth_key(uint64_t seed, const char *name);
+/* Q4_0 blocks: d = f16(|N(0, sigma)|), 16 uniform random bytes per block. */
+int cw_synth_q4(uint64_t key, size_t nblocks, float sigma, uint16_t *scales, uint8_t *quants);
+/* n f32 values ~ N(mean, std). */
+int cw_synth_normal_f32(uint64_t key, size_t n, float mean, float std, float *out);
+/* n f16 values ~ N(mean, std), rounded to nearest even. */
+int cw_synth_normal_f16(uint64_t key, size_t n, float mean, float std, uint16_t *out);
+/* n token ids uniform in [0, vocab). */
+int cw_synth_tokens(uint64_t key, size_t n, uint32_t vocab, uint32_t *out);
+
+/* ---------------------------------------------------------------- */
+/* Model: Qwen3 forward + greedy loop (src/model/NAME.rs)              */
+/* ---------------------------------------------------------------- */
+
+/* The per-family composition switches the reference pins for qwen3
+ * (README.md:47-63): plain RMSNorm gain, SwiGLU, per-head QK-norm, no QKV
+ * bias, LM head tied to the embedding unless "output.weight" is given. */
+typedef struct cw_family_spec {
+    int norm_unit_gain;  /* 0: y = x/rms * w (the only form built) */
+    int act;             /* 0: SwiGLU (the only form built) */
+    int qk_norm;         /* 1: per-head RMSNorm on q and k */
+    int qkv_bias;        /* 0: no bias (the only form built) */
+} cw_family_spec;
+
+/* The metadata Qwen3::load reads (src/model/qwen3.rs:45-53). */
+typedef struct cw_model_config {
+    cw_family_spec family;
+    int n_layers, dim, n_heads, n_kv_heads, head_dim, hidden, vocab;
+    float eps, rope_theta;
+    int max_seq;   /* KV capacity (Model::new_cache's max_seq, mod.rs:65) */
+    int kv_dtype;  /* CW_F32 or CW_F16 */
+} cw_model_config;
+
+/* Qwen3 (src/model/qwen3.rs:44-113): allocate device storage for every
+ * tensor and the KV cache.  Weights are then supplied by name. */
+int cw_model_create(cw_ctx *ctx, const cw_model_config *cfg, cw_model **out);
+int cw_model_destroy(cw_model *m);
+/* Weights::matrix_raw + Q4Linear (src/model/mod.rs:130-153, layers.rs:74-95),
+ * by GGUF name ("blk.3.attn_q.weight", "output.weight", ...). */
+int cw_model_set_q4(cw_model *m, const char *name, const uint16_t *scales_host,
+                    const uint8_t *quants_host);
+/* Weights::vector (norm gains "blk.3.attn_norm.weight", "output_norm.weight";
+ * the embedding "token_embd.weight" [vocab][dim]). */
+int cw_model_set_f32(cw_model *m, const char *name, const float *data_host);
+/* Every tensor of the config's distributions generated from seed by the
+ * cw_synth_* functions under its GGUF name (host side, then uploaded). */
+int cw_model_load_synthetic(cw_model *m, uint64_t seed);
+/* Checks every tensor is present; builds the tied LM head (qwen3.rs:93-98)
+ * when "output.weight" was not given. */
+int cw_model_finalize(cw_model *m);
+/* Fill KV positions [0, n_pos) of every layer from host arrays laid out
+ * [layer][pos][kv_dim] in the cache's element type. */
+int cw_model_prefill_kv(cw_model *m, const void *k_host, const void *v_host, int n_pos);
+/* One forward at pos for token (embed -> forward -> logits -> argmax), the
+ * body of generate's loop (src/model/mod.rs:93-103).  Returns the argmax. */
+int cw_model_step(cw_model *m, uint32_t token, int pos, uint32_t *argmax_out);
+/* Download the logits [vocab] of the last step. */
+int cw_model_logits(cw_model *m, float *host_out);
+/* Download the final hidden state [dim] (post final norm) of the last step. */
+int cw_model_hidden(cw_model *m, float *host_out);
+/* model::generate (src/model/mod.rs:57-125): greedy loop over the prompt then
+ * max_new produced tokens (P+N-1 forwards), the whole step device-resident
+ * (position and token live on the device) and replayed as a HIP graph when
+ * use_graph != 0.  The first prompt token is fed at start_pos (0 = empty
+ * cache).  Writes max_new ids to out_tokens. */
+int cw_generate(cw_model *m, const uint32_t *prompt, int n_prompt, int max_new, int start_pos,
+                int use_graph, uint32_t *out_tokens);
+/* Launch n_steps more decode steps of the current generate state without
+ * synchronising (for timing); cw_flush waits. */
+int cw_model_decode_async(cw_model *m, int n_steps, int use_graph);
+/* Reset the decode state to (token, pos) without touching the cache. */
+int cw_model_reset_state(cw_model *m, uint32_t token, int pos);
+/* Download the tokens produced so far by the device-resident loop. */
+int cw_model_tokens(cw_model *m, uint32_t *host_out, int max_n, int *n_out);
+
+/* ---------------------------------------------------------------- */
+/* Profiling (src/profile.rs, GpuContext::begin_profile/report_profile) */
+/* ---------------------------------------------------------------- */
+
+/* Start recording a HIP event pair around every launch, labelled by kernel. */
+int cw_profile_begin(cw_ctx *ctx);
+/* Synchronise, stop recording and write a table "label count total_ms" (one
+ * label per line, like profile.rs:121-134) into buf. */
+int cw_profile_report(cw_ctx *ctx, char *buf, size_t buf_len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CHAT_WGPU_H */

@@ -1,0 +1,356 @@
+"""Pins the CPU oracle (oracle/cw_oracle.c) against the reference's own known
+answers (tests/golden/reference_kats.json), independent implementations
+(numpy), closed forms and f64 truth.  CPU only."""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle as orc
+from conftest import GOLDEN
+
+with open(os.path.join(GOLDEN, "reference_kats.json")) as f:
+    KATS = json.load(f)
+
+
+def f32bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+# ---------------------------------------------------------------- f16 / Q4_0 unpack
+
+def test_f16_kat():
+    for h, v in KATS["f16_to_f32"]["cases"]:
+        assert orc.f16_to_f32(h) == v
+
+
+def test_f16_to_f32_exhaustive_vs_numpy():
+    lib = orc.lib()
+    pats = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ours = np.array([lib.or_f16_to_f32(int(h)) for h in pats], np.float32)
+    ref = pats.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(f32bits(ours[~nan]), f32bits(ref[~nan]))
+    # dequant.rs:16: NaN patterns become f32::NAN with the sign applied by negation
+    sign = (pats[nan] >> 15).astype(np.uint32)
+    assert np.all(np.isnan(ours[nan]))
+    assert np.array_equal(f32bits(ours[nan]), (sign << 31) | 0x7FC00000)
+
+
+def test_f32_to_f16_vs_numpy(rng):
+    lib = orc.lib()
+    vals = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(10.0) ** rng.integers(-9, 6, 20000),
+        # every f16 value and the midpoints between neighbours (ties -> even)
+        np.arange(0, 0x7C00, 7, dtype=np.uint16).view(np.float16).astype(np.float32),
+        (np.arange(0, 0x7BFF, 13, dtype=np.uint16).view(np.float16).astype(np.float64) / 2 +
+         np.arange(1, 0x7C00, 13, dtype=np.uint16).view(np.float16).astype(np.float64) / 2
+         ).astype(np.float32),
+        np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 1e-8, 2.0 ** -25, 2.0 ** -24,
+                  3 * 2.0 ** -26, np.inf, -np.inf], np.float32)])
+    ours = np.array([lib.or_f32_to_f16(float(v)) for v in vals], np.uint16)
+    ref = vals.astype(np.float16).view(np.uint16)
+    assert np.array_equal(ours, ref)
+
+
+def test_q4_0_block_kat():
+    k = KATS["q4_0_block"]
+    blk = np.array([k["d"] & 0xFF, k["d"] >> 8] + [k["byte"]] * 16, np.uint8)
+    out = orc.dequant_q4_0(blk, 32)
+    for idx, v in k["expect"].items():
+        assert out[int(idx)] == v
+    # the KAT pins GGUF nibble order: low nibble -> j, high nibble -> j+16
+    assert np.all(out[:16] == 0.0) and np.all(out[16:] == 7.0)
+
+
+def test_dequant_brute_force_all_scales_and_nibbles():
+    """Every f16 scale pattern x every nibble at every position of a block,
+    against numpy's float16 conversion times (q-8) in f32."""
+    d = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    finite = np.isfinite(d.view(np.float16))
+    d = d[finite]
+    n = d.size
+    # byte j of block b: low nibble (b+j)%16, high nibble (b+3j+5)%16
+    b = np.arange(n)[:, None]
+    j = np.arange(16)[None, :]
+    lo = (b + j) % 16
+    hi = (b + 3 * j + 5) % 16
+    qs = (lo | (hi << 4)).astype(np.uint8)
+    blocks = np.concatenate([d.view(np.uint8).reshape(n, 2), qs], axis=1)
+    out = orc.dequant_q4_0(blocks, n * 32).reshape(n, 32)
+    df = d.view(np.float16).astype(np.float32)[:, None]
+    exp = np.concatenate([df * (lo - 8).astype(np.float32), df * (hi - 8).astype(np.float32)], 1)
+    assert np.array_equal(f32bits(out), f32bits(exp))
+    soa = orc.dequant_q4_0_soa(d, qs).reshape(n, 32)
+    assert np.array_equal(f32bits(soa), f32bits(out))
+
+
+# ---------------------------------------------------------------- re-quantizer
+
+def _block_on_grid(rng, d, n_rows, in_f):
+    q = rng.integers(0, 16, (n_rows, in_f)).astype(np.int32)
+    q[:, ::32] = 0  # every block holds a -8*d element, so absmax = 8d
+    return (d * (q - 8)).astype(np.float32), q
+
+
+def test_quantize_q4_0_exact_grid_round_trip(rng):
+    d = np.float32(0.0078125)  # 2^-7: exact in f32 and f16
+    data, q = _block_on_grid(rng, d, 8, 128)
+    s, words = orc.quantize_q4_0(data)
+    assert np.all(s == d)
+    nib = np.stack([(words >> (4 * n)) & 15 for n in range(8)], -1).reshape(8, 128)
+    assert np.array_equal(nib, q)
+    gs, gq = orc.quantize_q4_0_gguf(data)
+    assert np.all(gs.view(np.float16).astype(np.float32) == d)
+    lo = (gq & 15).astype(np.int32)
+    hi = (gq >> 4).astype(np.int32)
+    assert np.array_equal(np.concatenate([lo, hi], -1).reshape(8, 128), q)
+
+
+def test_quantize_q4_0_rounding_and_clamp():
+    blk = np.zeros((1, 32), np.float32)
+    blk[0, 0] = 8.0          # absmax 8 -> d = 1
+    blk[0, 1] = 2.5          # Rust round: half away from zero -> 3 -> q = 11
+    blk[0, 2] = -2.5         # -> -3 -> q = 5
+    blk[0, 3] = -8.0         # q = 0
+    blk[0, 4] = 0.49999997   # -> 0 -> q = 8
+    s, words = orc.quantize_q4_0(blk)
+    nib = [(int(words[0, 0]) >> (4 * n)) & 15 for n in range(8)]
+    assert s[0, 0] == 1.0
+    assert nib[:5] == [15, 11, 5, 0, 8]   # +8 clamps to 15
+    zero = np.zeros((1, 32), np.float32)
+    s, words = orc.quantize_q4_0(zero)
+    assert s[0, 0] == 0.0 and np.all(words == 0x88888888)
+
+
+def test_quantize_gguf_error_bound(rng):
+    data = rng.standard_normal((64, 256)).astype(np.float32) * 0.02
+    s, q = orc.quantize_q4_0_gguf(data)
+    deq = orc.dequant_q4_0_soa(s, q).reshape(64, 256)
+    d = s.view(np.float16).astype(np.float32).repeat(32, axis=1)
+    # inside the grid the rounding error is <= d/2; the +8 side clamps at 7d
+    err = np.abs(deq - data)
+    inside = data < 7.5 * d
+    assert np.all(err[inside] <= 0.5 * d[inside] * (1 + 1e-3) + 1e-12)
+
+
+# ---------------------------------------------------------------- GEMV / matmul
+
+def test_q4_gemv_kat_fixture():
+    z = np.load(os.path.join(GOLDEN, "q4_gemv_kat.npz"))
+    k = KATS["q4_gemv"]
+    x = orc.fill(k["seed_x"], k["in_f"])
+    w = orc.fill(k["seed_w"], k["out_f"] * k["in_f"]).reshape(k["out_f"], k["in_f"])
+    assert np.array_equal(x, z["x"])
+    s, q = orc.quantize_q4_0(w)
+    assert np.array_equal(s, z["ref_scales"]) and np.array_equal(q, z["ref_quants"])
+    y = orc.q4_gemv_refmt(x, s, q, 256, 512)
+    assert np.array_equal(f32bits(y), f32bits(z["ref_y"]))
+    # independent check: numpy dequant of the reference layout, f64 dot
+    nib = np.stack([(q >> (4 * n)) & 15 for n in range(8)], -1).reshape(512, 256).astype(np.float64)
+    wd = (s.astype(np.float64).repeat(32, axis=1)) * (nib - 8.0)
+    y64 = wd @ x.astype(np.float64)
+    assert np.max(np.abs(y - y64)) <= 1e-5 * np.max(np.abs(y64))
+    gy = orc.q4_gemv(x, z["gguf_scales"], z["gguf_quants"], 256, 512)
+    assert np.array_equal(f32bits(gy), f32bits(z["gguf_y"]))
+
+
+def test_q4_gemv_closed_forms(rng):
+    out_f, in_f = 48, 256
+    s = rng.random((out_f, in_f // 32)).astype(np.float16).view(np.uint16)
+    x = rng.standard_normal(in_f).astype(np.float32)
+    # all nibbles 8 -> exactly zero (the q4bench/q4trace input 0x88888888)
+    q8 = np.full((out_f, in_f // 32, 16), 0x88, np.uint8)
+    assert np.all(orc.q4_gemv(x, s, q8, in_f, out_f) == 0.0)
+    # one-hot x -> the dequantized column, bit for bit
+    q = rng.integers(0, 256, (out_f, in_f // 32, 16)).astype(np.uint8)
+    deq = orc.dequant_q4_0_soa(s, q).reshape(out_f, in_f)
+    for k in (0, 15, 16, 31, 32, 200, 255):
+        e = np.zeros(in_f, np.float32)
+        e[k] = 1.0
+        y = orc.q4_gemv(e, s, q, in_f, out_f)
+        assert np.array_equal(f32bits(y), f32bits(deq[:, k] + np.float32(0.0)))
+    # constant q = c with d = 1 -> (c - 8) * sum(x) (integer x: exact)
+    xi = rng.integers(-4, 5, in_f).astype(np.float32)
+    ones = np.full((out_f, in_f // 32), 0x3C00, np.uint16)
+    for c in (0, 3, 15):
+        qc = np.full((out_f, in_f // 32, 16), c | (c << 4), np.uint8)
+        y = orc.q4_gemv(xi, ones, qc, in_f, out_f)
+        assert np.all(y == (c - 8) * xi.sum())
+
+
+def test_q4_gemv_vs_f64_truth(rng):
+    out_f, in_f = 300, 3072
+    s = (np.abs(rng.standard_normal((out_f, in_f // 32))) * 0.02).astype(np.float16).view(np.uint16)
+    q = rng.integers(0, 256, (out_f, in_f // 32, 16)).astype(np.uint8)
+    x = rng.standard_normal(in_f).astype(np.float32)
+    y = orc.q4_gemv(x, s, q, in_f, out_f)
+    y64, absy = orc.q4_gemv_f64(x, s, q, in_f, out_f)
+    deq = orc.dequant_q4_0_soa(s, q).reshape(out_f, in_f).astype(np.float64)
+    assert np.allclose(deq @ x.astype(np.float64), y64, rtol=1e-12, atol=1e-12)
+    assert np.all(np.abs(y - y64) <= 1e-5 * absy)
+
+
+def test_naive_matmul(rng):
+    m, k, n = 8, 1024, 32
+    c = orc.naive_matmul(np.ones(m * k), np.ones(k * n), m, k, n)
+    assert np.all(c == k)  # main.rs:53-59
+    a = rng.standard_normal((3, 77)).astype(np.float32)
+    b = rng.standard_normal((77, 5)).astype(np.float32)
+    c = orc.naive_matmul(a, b, 3, 77, 5).reshape(3, 5)
+    assert np.allclose(c, a.astype(np.float64) @ b.astype(np.float64), rtol=1e-5, atol=1e-5)
+
+
+# ---------------------------------------------------------------- norm / rope / attention
+
+def test_rmsnorm_kat_and_truth(rng):
+    k = KATS["rmsnorm_ones"]
+    y = orc.rmsnorm(np.ones(k["rows"] * k["dim"]), np.ones(k["dim"]), k["rows"], k["dim"], k["eps"])
+    assert np.max(np.abs(y - 1.0 / math.sqrt(1.0 + k["eps"]))) < 1e-6
+    x = rng.standard_normal((5, 128)).astype(np.float32)
+    w = rng.standard_normal(128).astype(np.float32)
+    y = orc.rmsnorm(x, w, 5, 128, 1e-6).reshape(5, 128)
+    x64 = x.astype(np.float64)
+    t = x64 / np.sqrt((x64 ** 2).mean(1, keepdims=True) + 1e-6) * w
+    assert np.allclose(y, t, rtol=2e-6, atol=1e-6)
+    # scale invariance (eps negligible against the mean square)
+    y2 = orc.rmsnorm(x * 8.0, w, 5, 128, 1e-6).reshape(5, 128)
+    assert np.allclose(y, y2, rtol=1e-5, atol=1e-6)
+
+
+def test_rope_pos0_identity_and_invariants(rng):
+    k = KATS["rope_pos0"]
+    x = (((np.arange(k["rows"] * k["head_dim"]) % 23) - 11) * 0.07).astype(np.float32)
+    y = orc.rope(x, k["rows"], k["head_dim"], 0, k["theta"])
+    assert np.array_equal(y, x)  # cos 0 = 1, sin 0 = 0: exact
+    hd, theta = 128, 1e6
+    q = rng.standard_normal(hd).astype(np.float32)
+    kk = rng.standard_normal(hd).astype(np.float32)
+    for pos in (1, 17, 4351):
+        r = orc.rope(q, 1, hd, pos, theta)
+        h = hd // 2
+        n0 = q[:h] ** 2 + q[h:] ** 2
+        n1 = r[:h] ** 2 + r[h:] ** 2
+        assert np.allclose(n0, n1, rtol=1e-5, atol=1e-6)
+    # <R_p q, R_r k> depends only on p - r
+    d1 = np.dot(orc.rope(q, 1, hd, 40, theta).astype(np.float64), orc.rope(kk, 1, hd, 10, theta))
+    d2 = np.dot(orc.rope(q, 1, hd, 530, theta).astype(np.float64), orc.rope(kk, 1, hd, 500, theta))
+    assert abs(d1 - d2) < 1e-4 * (1 + abs(d1))
+
+
+def test_rope_table_vs_numpy_and_f32_literal(rng):
+    hd, theta = 128, 1e6
+    c, s = orc.rope_table(4352, hd, theta)
+    i = np.arange(hd // 2)
+    p = np.arange(4352)[:, None].astype(np.float64)
+    f = p * np.power(float(np.float32(theta)), -2.0 * i / hd)
+    # same f64 formula, numpy's libm: equal to within one f32 ulp
+    assert np.max(np.abs(c - np.cos(f).astype(np.float32))) <= 1.2e-7
+    assert np.max(np.abs(s - np.sin(f).astype(np.float32))) <= 1.2e-7
+    # the reference's literal f32 formula drifts by ~pos * ulp(freq)
+    x = rng.standard_normal(hd).astype(np.float32)
+    for pos in (0, 1, 100):
+        a = orc.rope(x, 1, hd, pos, theta)
+        b = orc.rope_f32_literal(x, 1, hd, pos, theta)
+        assert np.max(np.abs(a - b)) < 1e-4 * max(1, pos)
+
+
+def test_attention_kats_and_truth(rng):
+    k = KATS["attention_seq1"]
+    nh, nkv, hd = k["n_heads"], k["n_kv"], k["head_dim"]
+    q = (np.arange(nh * hd) * 0.01).astype(np.float32)
+    v = (((np.arange(nkv * hd) % 9) - 4) * 0.1).astype(np.float32)
+    kc = np.full(nkv * hd, 0.5, np.float32)
+    o = orc.attention(q, kc, v, False, nh, nkv, 1, hd).reshape(nh, hd)
+    for h in range(nh):
+        assert np.max(np.abs(o[h] - v.reshape(nkv, hd)[h // (nh // nkv)])) < 1e-6
+    # constant K -> uniform softmax -> mean of V
+    seq = 77
+    kc = np.tile(rng.standard_normal(nkv * hd).astype(np.float32), seq)
+    vv = rng.standard_normal(seq * nkv * hd).astype(np.float32)
+    o = orc.attention(q, kc, vv, False, nh, nkv, seq, hd).reshape(nh, hd)
+    mean = vv.reshape(seq, nkv, hd).astype(np.float64).mean(0)
+    for h in range(nh):
+        assert np.allclose(o[h], mean[h // 2], atol=2e-6)
+    # against the f64 two-pass softmax, f32 and f16 caches
+    for kv16 in (False, True):
+        nh, nkv, hd, seq = 8, 2, 64, 300
+        q = rng.standard_normal(nh * hd).astype(np.float32)
+        kr = rng.standard_normal(seq * nkv * hd).astype(np.float32)
+        vr = rng.standard_normal(seq * nkv * hd).astype(np.float32)
+        if kv16:
+            kr = kr.astype(np.float16).view(np.uint16)
+            vr = vr.astype(np.float16).view(np.uint16)
+        o = orc.attention(q, kr, vr, kv16, nh, nkv, seq, hd)
+        o64 = orc.attention_f64(q, kr, vr, kv16, nh, nkv, seq, hd)
+        assert np.max(np.abs(o - o64)) < 2e-5
+
+
+def test_swiglu_add_kats():
+    k = KATS["swiglu_const"]
+    g = np.float32(k["g"])
+    u = np.float32(k["u"])
+    out = orc.swiglu(np.full(k["n"], g), np.full(k["n"], u))
+    exp = np.float32(g / (np.float32(1.0) + np.exp(-g, dtype=np.float32)) * u)
+    assert np.max(np.abs(out - exp)) < 1e-6
+    n = KATS["ewise_add"]["n"]
+    a = np.arange(n, dtype=np.float32)
+    b = -np.arange(n, dtype=np.float32) * np.float32(0.5)
+    assert np.array_equal(orc.add(a, b), a + b)
+
+
+def test_argmax_rules(rng):
+    x = rng.standard_normal(151936).astype(np.float32)
+    assert orc.argmax(x) == int(np.argmax(x))
+    x[10] = x[20] = x[30] = 100.0
+    assert orc.argmax(x) == 10  # ties -> lowest index
+    x[5] = np.nan
+    assert orc.argmax(x) == 10  # NaN never wins
+    assert orc.argmax(np.full(9, -np.inf, np.float32)) == 0
+
+
+# ---------------------------------------------------------------- seeded test data
+
+def test_fill_and_seed_restatement():
+    # FNV-1a 64 (main.rs:253-255) and the LCG (main.rs:257-266) in Python ints
+    def fnv(name):
+        h = 1469598103934665603
+        for ch in name.encode():
+            h = ((h ^ ch) * 1099511628211) % (1 << 64)
+        return h
+
+    for name in ("blk.0.attn_q.weight", "token_embd.weight", ""):
+        assert orc.fnv_seed(name) == fnv(name)
+    seed, n = 0x1234, 1000
+    s = seed | 1
+    exp = []
+    for _ in range(n):
+        s = (s * 6364136223846793005 + 1442695040888963407) % (1 << 64)
+        v = np.float32(np.float32(s >> 33) / np.float32(4294967295.0))
+        exp.append(np.float32((v - np.float32(0.5)) * np.float32(0.2)))
+    got = orc.fill(seed, n)
+    assert np.array_equal(got, np.array(exp, np.float32))
+    big = orc.fill(0x5678, 200000)
+    assert big.min() >= -0.1 and big.max() < 0.0  # the [-0.1, 0) quirk
+
+
+def test_tiny_model_fixture():
+    """The reference verify-model shape, RandomWeights, Q4: the greedy loop is
+    deterministic and equals the committed fixture; P+N-1 forwards."""
+    import make_golden as mg
+    z = np.load(os.path.join(GOLDEN, "tiny_qwen3.npz"))
+    w = mg.tiny_weights()
+    m = orc.OracleModel(mg.TinyCfg, w)
+    toks, margins = m.generate(np.array([1, 5, 9, 2], np.uint32), 8)
+    assert np.array_equal(toks, z["tokens"])
+    m2 = orc.OracleModel(mg.TinyCfg, w)
+    logits, _ = m2.step(1, 0)
+    assert np.array_equal(f32bits(logits), f32bits(z["logits_tok1_pos0"]))
+    # the first produced token is the argmax after the last prompt position
+    m3 = orc.OracleModel(mg.TinyCfg, w)
+    for pos, t in enumerate([1, 5, 9]):
+        m3.step(t, pos)
+    lg, _ = m3.step(2, 3)
+    assert orc.argmax(lg) == toks[0]
