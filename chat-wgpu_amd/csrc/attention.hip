@@ -3,44 +3,66 @@
 // Replaces attention::attention (src/kernels/attention.rs:7-38,
 // attention.wgsl:23-96).  Same mathematics: o_h = sum_j softmax_j(scale *
 // q_h . k_j) v_j over j < seq, kv head = h / (n_heads / n_kv), scale =
-// hd^-0.5, online (max-rescaled) softmax.
+// hd^-0.5, max-rescaled softmax.
 //
-// Split over the sequence (flash-decoding): workgroup (chunk c, kv head g)
-// covers 128 positions with 4 waves of 32.  Every kv head's K/V rows are
-// read once for all its GQA query heads.  A wave reads 4 positions per step,
-// 16 lanes per row (coalesced 16-byte loads of a position's head slice),
-// reduces q.k within each 16-lane row with DPP, keeps a per-wave
-// (max, sum, acc) and the 4 waves merge through LDS.  A second kernel merges
-// the chunk partials.
+// Split over the sequence (flash-decoding).  Workgroup (chunk c, kv head g)
+// owns CP consecutive positions and one wave per query head of the GQA group:
+//   1. the K and V rows of the chunk (this kv head's slice) are loaded with
+//      coalesced 16-byte loads, all issued up front, into an LDS tile with a
+//      16-byte row pad (conflict-free row reads);
+//   2. wave j: lane = position, full q.k dot from the LDS tile against the
+//      query broadcast from LDS (f16 keys feed v_fma_mix directly);
+//      wavefront max / sum give the chunk's softmax partial;
+//   3. wave j: lane = head dimension, P.V over the tile's rows.
+// No cross-lane reduction is needed per position.  A chunk partial
+// (max, sum, unnormalised o) goes to HBM unless the sequence fits one chunk,
+// in which case the normalised output is written directly; the merge kernel
+// combines chunks with one round of independent loads.
 //
 // Fused prologue (decode step): the raw q/k/v come straight from the fused
 // QKV projection; the kernel applies the per-head QK RMSNorm (norm.wgsl,
-// qwen3.rs:154-155) and RoPE (rope.wgsl) and the workgroup whose chunk holds
-// the new position writes k/v into the cache (cache.rs:21-24), substituting
-// the new row from LDS for its own use.
+// qwen3.rs:154-155) and RoPE (rope.wgsl), and the workgroup whose chunk holds
+// the new position writes k/v into the cache (cache.rs:21-24) and into its
+// own tile.
 
 #include <cmath>
+#include <map>
+#include <mutex>
 
 #include "cw_internal.hpp"
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kChunk = 128;  // positions per workgroup
-constexpr int kPerWave = 32;
-constexpr int kSteps = kPerWave / 4;
+constexpr int kMaxChunkSpan = 32768;  // max_seq limit
+constexpr int kMergeThreads = 256;
 
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-    return __builtin_bit_cast(
-        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
+template <typename KVT, int HD, int HPK>
+struct Cfg {
+    static constexpr int ES = (int)sizeof(KVT);
+    static constexpr int THREADS = 64 * HPK;
+    // 16-byte loads per thread for the K+V tile.  Chunks of <= 64 positions
+    // keep the tile near 36 KB so several workgroups share a CU and every
+    // chunk of a 4K-position cache is resident at once (8 kv heads x 68
+    // chunks = 544 workgroups); small groups load more per thread.
+    static constexpr int LB = THREADS <= 128 ? 32 : 8;
+    static constexpr int CP0 = LB * THREADS * 16 / (2 * HD * ES);
+    static constexpr int CP = CP0 > 64 ? 64 : CP0;  // positions per workgroup
+    static constexpr int ROWB = HD * ES;              // bytes of one row slice
+    static constexpr int ROWP = ROWB + 16;            // padded LDS row stride
+    static constexpr int U4_ROW = ROWB / 16;          // 16-byte units per row
+    static constexpr int NLOAD = (CP * U4_ROW + THREADS - 1) / THREADS;
+    static constexpr int NT = (CP + 63) / 64;         // positions per lane
+    static constexpr int DPL = HD >= 64 ? HD / 64 : 1;  // dims per lane in P.V
+    static constexpr int EPU = 16 / ES;               // elements per 16 bytes
+    // LDS: K tile, V tile, q [HPK][HD], p [HPK][CP]
+    static constexpr int LDS = 2 * CP * ROWP + HPK * HD * 4 + HPK * CP * 4;
+    static_assert(LDS <= 160 * 1024, "attention tile exceeds the CU's LDS");
+    static_assert(CP >= 8 && CP % 8 == 0, "chunk must hold whole load groups");
+};
 
-__device__ __forceinline__ float sum16(float v) {
-    v += dpp<0xB1>(v);
-    v += dpp<0x4E>(v);
-    v += dpp<0x141>(v);
-    v += dpp<0x140>(v);
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
     return v;
 }
 
@@ -51,260 +73,412 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 template <typename T>
-__device__ __forceinline__ float kv_f(T v) {
-    return (float)v;
-}
-
-template <typename T>
 __device__ __forceinline__ T to_kv(float v) {
     return (T)v;  // f32 -> f16 rounds to nearest even
 }
 
-template <typename T, int N>
-struct alignas((sizeof(T) * N) >= 16 ? 16 : (sizeof(T) * N)) Vec {
-    T v[N];
-};
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
-template <typename T, int N>
-__device__ __forceinline__ Vec<T, N> load_vec(const T *p) {
-    return *reinterpret_cast<const Vec<T, N> *>(p);
+// sum over the elements of one 16-byte unit of a K row times q (f32)
+template <typename KVT>
+__device__ __forceinline__ float dot16(uint4 k, const float *q, float acc);
+
+template <>
+__device__ __forceinline__ float dot16<_Float16>(uint4 k, const float *q, float acc) {
+    const uint32_t w[4] = {k.x, k.y, k.z, k.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const half2v h = __builtin_bit_cast(half2v, w[i]);
+        acc = __builtin_fmaf((float)h.x, q[2 * i], acc);
+        acc = __builtin_fmaf((float)h.y, q[2 * i + 1], acc);
+    }
+    return acc;
+}
+
+template <>
+__device__ __forceinline__ float dot16<float>(uint4 k, const float *q, float acc) {
+    acc = __builtin_fmaf(__builtin_bit_cast(float, k.x), q[0], acc);
+    acc = __builtin_fmaf(__builtin_bit_cast(float, k.y), q[1], acc);
+    acc = __builtin_fmaf(__builtin_bit_cast(float, k.z), q[2], acc);
+    acc = __builtin_fmaf(__builtin_bit_cast(float, k.w), q[3], acc);
+    return acc;
 }
 
 template <typename KVT, int HD, int HPK>
-__global__ __launch_bounds__(kThreads) void attn_partial_kernel(cwi::AttnArgs a, float scale,
-                                                                int max_chunks) {
-    constexpr int EPL = HD / 16;  // elements per lane
+__global__ __launch_bounds__(64 * HPK) void attn_kernel(cwi::AttnArgs a, float scale,
+                                                        int max_chunks) {
+    using C = Cfg<KVT, HD, HPK>;
     constexpr int HALF = HD / 2;
+    extern __shared__ uint4 lds_u4[];
+    unsigned char *lds = reinterpret_cast<unsigned char *>(lds_u4);
+    unsigned char *k_t = lds;                       // [CP][ROWP]
+    unsigned char *v_t = lds + C::CP * C::ROWP;     // [CP][ROWP]
+    float *q_s = reinterpret_cast<float *>(lds + 2 * C::CP * C::ROWP);  // [HPK][HD]
+    float *p_s = q_s + HPK * HD;                                       // [HPK][CP]
+
     const int c = blockIdx.x, g = blockIdx.y;
     const int seq = a.pos_dev ? (*a.pos_dev + 1) : a.seq;
-    const int c0 = c * kChunk;
+    const int c0 = c * C::CP;
     if (c0 >= seq) return;
+    const int n_chunks = (seq + C::CP - 1) / C::CP;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int dg = lane & 15, pg = lane >> 4;
     const int kv_dim = a.n_kv * HD;
     const bool fused = a.qkv != nullptr;
     const int pos_new = seq - 1;
-    const bool has_new = fused && pos_new >= c0 && pos_new < c0 + kChunk;
-    KVT *kc = reinterpret_cast<KVT *>(a.k_cache);
-    KVT *vc = reinterpret_cast<KVT *>(a.v_cache);
+    const bool has_new = fused && pos_new >= c0 && pos_new < c0 + C::CP;
+    const unsigned char *kc = reinterpret_cast<const unsigned char *>(a.k_cache);
+    const unsigned char *vc = reinterpret_cast<const unsigned char *>(a.v_cache);
+    const size_t row_bytes = (size_t)kv_dim * C::ES;
 
-    __shared__ float q_s[HPK][HD];
-    __shared__ float knew_s[HD], vnew_s[HD];
-    __shared__ float w_o[4][HPK][HD];
-    __shared__ float w_m[4][HPK], w_l[4][HPK];
+    // ---- 1. issue the K/V tile loads ----
+    uint4 kr[C::NLOAD], vr[C::NLOAD];
+#pragma unroll
+    for (int i = 0; i < C::NLOAD; ++i) {
+        const int f = tid + i * C::THREADS;
+        const int row = f / C::U4_ROW, col = f % C::U4_ROW;
+        int p = c0 + row;
+        p = p < seq ? p : seq - 1;
+        const size_t off = (size_t)p * row_bytes + (size_t)g * C::ROWB + (size_t)col * 16;
+        if (f < C::CP * C::U4_ROW) {
+            kr[i] = *reinterpret_cast<const uint4 *>(kc + off);
+            vr[i] = *reinterpret_cast<const uint4 *>(vc + off);
+        }
+    }
 
-    // ---- query heads (and the new k/v row) ----
-    if (fused) {
-        const int q_dim = a.n_heads * HD;
-        for (int j = wave; j < HPK + 2; j += 4) {
-            if (j >= HPK && !has_new) continue;
-            if (j == HPK + 1) {  // v: plain copy, rounded to the cache type
-                for (int i = lane; i < HD; i += 64)
-                    vnew_s[i] = kv_f(to_kv<KVT>(a.qkv[q_dim + kv_dim + g * HD + i]));
-                continue;
-            }
-            const float *src = j < HPK ? a.qkv + (size_t)(g * HPK + j) * HD : a.qkv + q_dim + g * HD;
-            const float *nw = j < HPK ? a.q_norm_w : a.k_norm_w;
+    // ---- 2. query head of this wave (normalised + rotated when fused) ----
+    float knew[(HALF + 63) / 64][2], vnew[(HD + 63) / 64];
+    {
+        const int h = g * HPK + wave;
+        if (fused) {
+            const float *src = a.qkv + (size_t)h * HD;
+            float lo[(HALF + 63) / 64], hi[(HALF + 63) / 64], cs[(HALF + 63) / 64],
+                sn[(HALF + 63) / 64];
             float ss = 0.0f;
-            for (int i = lane; i < HD; i += 64) ss += src[i] * src[i];
+#pragma unroll
+            for (int u = 0; u < (HALF + 63) / 64; ++u) {
+                const int i = lane + 64 * u;
+                lo[u] = hi[u] = cs[u] = sn[u] = 0.0f;
+                if (i < HALF) {
+                    lo[u] = src[i];
+                    hi[u] = src[i + HALF];
+                    cs[u] = a.cos_t[(size_t)pos_new * HALF + i];
+                    sn[u] = a.sin_t[(size_t)pos_new * HALF + i];
+                    ss += lo[u] * lo[u] + hi[u] * hi[u];
+                }
+            }
             ss = wave_sum(ss);
             const float inv = 1.0f / sqrtf(ss / (float)HD + a.eps);
-            for (int i = lane; i < HALF; i += 64) {
-                const float lo = (src[i] * inv) * nw[i];
-                const float hi = (src[i + HALF] * inv) * nw[i + HALF];
-                const float cs = a.cos_t[(size_t)pos_new * HALF + i];
-                const float sn = a.sin_t[(size_t)pos_new * HALF + i];
-                const float y0 = lo * cs - hi * sn;
-                const float y1 = hi * cs + lo * sn;
-                if (j < HPK) {
-                    q_s[j][i] = y0;
-                    q_s[j][i + HALF] = y1;
-                } else {
-                    knew_s[i] = kv_f(to_kv<KVT>(y0));
-                    knew_s[i + HALF] = kv_f(to_kv<KVT>(y1));
+#pragma unroll
+            for (int u = 0; u < (HALF + 63) / 64; ++u) {
+                const int i = lane + 64 * u;
+                if (i < HALF) {
+                    const float l0 = (lo[u] * inv) * a.q_norm_w[i];
+                    const float h0 = (hi[u] * inv) * a.q_norm_w[i + HALF];
+                    q_s[wave * HD + i] = l0 * cs[u] - h0 * sn[u];
+                    q_s[wave * HD + i + HALF] = h0 * cs[u] + l0 * sn[u];
+                }
+            }
+            if (has_new && wave == 0) {  // the new k (normed + rotated) and v
+                const int q_dim = a.n_heads * HD;
+                const float *ks = a.qkv + q_dim + g * HD;
+                const float *vs = a.qkv + q_dim + kv_dim + g * HD;
+                float kss = 0.0f;
+                float klo[(HALF + 63) / 64], khi[(HALF + 63) / 64];
+#pragma unroll
+                for (int u = 0; u < (HALF + 63) / 64; ++u) {
+                    const int i = lane + 64 * u;
+                    klo[u] = khi[u] = 0.0f;
+                    if (i < HALF) {
+                        klo[u] = ks[i];
+                        khi[u] = ks[i + HALF];
+                        kss += klo[u] * klo[u] + khi[u] * khi[u];
+                    }
+                }
+                kss = wave_sum(kss);
+                const float kinv = 1.0f / sqrtf(kss / (float)HD + a.eps);
+#pragma unroll
+                for (int u = 0; u < (HALF + 63) / 64; ++u) {
+                    const int i = lane + 64 * u;
+                    if (i < HALF) {
+                        const float l0 = (klo[u] * kinv) * a.k_norm_w[i];
+                        const float h0 = (khi[u] * kinv) * a.k_norm_w[i + HALF];
+                        knew[u][0] = l0 * cs[u] - h0 * sn[u];
+                        knew[u][1] = h0 * cs[u] + l0 * sn[u];
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < (HD + 63) / 64; ++u) {
+                    const int i = lane + 64 * u;
+                    vnew[u] = i < HD ? vs[i] : 0.0f;
+                }
+            }
+        } else {
+            for (int i = lane; i < HD; i += 64) q_s[wave * HD + i] = a.q[(size_t)h * HD + i];
+        }
+    }
+
+    // ---- 3. tile -> LDS (rows past the sequence as zeros; the new row from
+    // registers, also to the cache) ----
+#pragma unroll
+    for (int i = 0; i < C::NLOAD; ++i) {
+        const int f = tid + i * C::THREADS;
+        if (f < C::CP * C::U4_ROW) {
+            const int row = f / C::U4_ROW, col = f % C::U4_ROW;
+            const bool live = c0 + row < seq;
+            const uint4 zero = make_uint4(0, 0, 0, 0);
+            *reinterpret_cast<uint4 *>(k_t + row * C::ROWP + col * 16) = live ? kr[i] : zero;
+            *reinterpret_cast<uint4 *>(v_t + row * C::ROWP + col * 16) = live ? vr[i] : zero;
+        }
+    }
+    __syncthreads();
+    if (has_new && wave == 0) {
+        const int r = pos_new - c0;
+        KVT *kt = reinterpret_cast<KVT *>(k_t + r * C::ROWP);
+        KVT *vt = reinterpret_cast<KVT *>(v_t + r * C::ROWP);
+        KVT *kg = reinterpret_cast<KVT *>(const_cast<unsigned char *>(kc) +
+                                          (size_t)pos_new * row_bytes + (size_t)g * C::ROWB);
+        KVT *vg = reinterpret_cast<KVT *>(const_cast<unsigned char *>(vc) +
+                                          (size_t)pos_new * row_bytes + (size_t)g * C::ROWB);
+#pragma unroll
+        for (int u = 0; u < (HALF + 63) / 64; ++u) {
+            const int i = lane + 64 * u;
+            if (i < HALF) {
+                const KVT k0 = to_kv<KVT>(knew[u][0]), k1 = to_kv<KVT>(knew[u][1]);
+                kt[i] = k0;
+                kt[i + HALF] = k1;
+                kg[i] = k0;
+                kg[i + HALF] = k1;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < (HD + 63) / 64; ++u) {
+            const int i = lane + 64 * u;
+            if (i < HD) {
+                const KVT v0 = to_kv<KVT>(vnew[u]);
+                vt[i] = v0;
+                vg[i] = v0;
+            }
+        }
+    }
+    if (has_new) __syncthreads();
+
+    // ---- 4. scores: lane = position ----
+    const float *qw = q_s + wave * HD;
+    constexpr int NA = C::U4_ROW >= 4 ? 4 : C::U4_ROW;  // independent partial sums
+    float s4[C::NT][NA];
+#pragma unroll
+    for (int t = 0; t < C::NT; ++t)
+#pragma unroll
+        for (int j = 0; j < NA; ++j) s4[t][j] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < C::U4_ROW; ++u) {
+        float qv[C::EPU];
+#pragma unroll
+        for (int e = 0; e < C::EPU; e += 4) {
+            const float4 q4 = *reinterpret_cast<const float4 *>(qw + u * C::EPU + e);
+            qv[e] = q4.x;
+            qv[e + 1] = q4.y;
+            qv[e + 2] = q4.z;
+            qv[e + 3] = q4.w;
+        }
+#pragma unroll
+        for (int t = 0; t < C::NT; ++t) {
+            const int r = lane + 64 * t;
+            if (r < C::CP) {
+                const uint4 kk = *reinterpret_cast<const uint4 *>(k_t + r * C::ROWP + u * 16);
+                s4[t][u % NA] = dot16<KVT>(kk, qv, s4[t][u % NA]);
+            }
+        }
+    }
+    float s[C::NT];
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < C::NT; ++t) {
+        float sv = s4[t][0];
+#pragma unroll
+        for (int j = 1; j < NA; ++j) sv += s4[t][j];
+        const int r = lane + 64 * t;
+        s[t] = (r < C::CP && c0 + r < seq) ? sv * scale : -INFINITY;
+        mloc = fmaxf(mloc, s[t]);
+    }
+    const float m = wave_max(mloc);  // finite: row c0 < seq exists
+    float lsum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < C::NT; ++t) {
+        const int r = lane + 64 * t;
+        const float pr = s[t] == -INFINITY ? 0.0f : expf(s[t] - m);
+        lsum += pr;
+        if (r < C::CP) p_s[wave * C::CP + r] = pr;
+    }
+    const float l = wave_sum(lsum);
+    __syncthreads();
+
+    // ---- 5. P.V: lane = head dimension, every tile row (masked rows carry
+    // p = 0 and a finite clamped V row), unrolled so LDS reads batch up ----
+    float o[C::DPL];
+    const int d0 = lane * C::DPL;
+    {
+        float o4[C::DPL][4];  // independent partial sums over rows
+#pragma unroll
+        for (int e = 0; e < C::DPL; ++e)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o4[e][j] = 0.0f;
+        if (d0 < HD) {
+            const float *pw = p_s + wave * C::CP;
+#pragma unroll
+            for (int r0 = 0; r0 < C::CP; r0 += 8) {
+                const float4 pa = *reinterpret_cast<const float4 *>(pw + r0);
+                const float4 pb = *reinterpret_cast<const float4 *>(pw + r0 + 4);
+                const float pr[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const KVT *vrow = reinterpret_cast<const KVT *>(v_t + (r0 + i) * C::ROWP) + d0;
+#pragma unroll
+                    for (int e = 0; e < C::DPL; ++e)
+                        o4[e][i & 3] = __builtin_fmaf(pr[i], (float)vrow[e], o4[e][i & 3]);
                 }
             }
         }
-    } else {
-        for (int idx = tid; idx < HPK * HD; idx += kThreads)
-            q_s[idx / HD][idx % HD] = a.q[(size_t)(g * HPK + idx / HD) * HD + idx % HD];
-    }
-    __syncthreads();
-    if (has_new) {
-        for (int i = tid; i < HD; i += kThreads) {
-            kc[(size_t)pos_new * kv_dim + g * HD + i] = to_kv<KVT>(knew_s[i]);
-            vc[(size_t)pos_new * kv_dim + g * HD + i] = to_kv<KVT>(vnew_s[i]);
-        }
+#pragma unroll
+        for (int e = 0; e < C::DPL; ++e) o[e] = (o4[e][0] + o4[e][1]) + (o4[e][2] + o4[e][3]);
     }
 
-    float qr[HPK][EPL];
+    // ---- 6. output (one chunk) or chunk partial ----
+    const int h = g * HPK + wave;
+    if (n_chunks == 1) {
+        const float inv = 1.0f / l;
+        if (d0 < HD)
 #pragma unroll
-    for (int j = 0; j < HPK; ++j)
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) qr[j][e] = q_s[j][dg * EPL + e];
-
-    // ---- stream this wave's 32 positions ----
-    const int wbase = c0 + wave * kPerWave;
-    Vec<KVT, EPL> kraw[kSteps], vraw[kSteps];
-#pragma unroll
-    for (int st = 0; st < kSteps; ++st) {
-        int p = wbase + st * 4 + pg;
-        p = p < seq ? p : seq - 1;
-        const size_t off = (size_t)p * kv_dim + g * HD + dg * EPL;
-        kraw[st] = load_vec<KVT, EPL>(kc + off);
-        vraw[st] = load_vec<KVT, EPL>(vc + off);
+            for (int e = 0; e < C::DPL; ++e) a.out[(size_t)h * HD + d0 + e] = o[e] * inv;
+        return;
     }
-
-    float s[kSteps][HPK];
+    float *po = a.part + ((size_t)h * max_chunks + c) * HD;
+    if (d0 < HD)
 #pragma unroll
-    for (int st = 0; st < kSteps; ++st) {
-        const int p = wbase + st * 4 + pg;
-        const bool is_new = has_new && p == pos_new;
-        float kf[EPL];
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) kf[e] = is_new ? knew_s[dg * EPL + e] : kv_f(kraw[st].v[e]);
-#pragma unroll
-        for (int j = 0; j < HPK; ++j) {
-            float part = 0.0f;
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) part = __builtin_fmaf(qr[j][e], kf[e], part);
-            part = sum16(part);
-            s[st][j] = p < seq ? part * scale : -INFINITY;
-        }
-    }
-
-    float m[HPK], l[HPK];
-#pragma unroll
-    for (int j = 0; j < HPK; ++j) {
-        float mx = s[0][j];
-#pragma unroll
-        for (int st = 1; st < kSteps; ++st) mx = fmaxf(mx, s[st][j]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        m[j] = mx;
-        float ls = 0.0f;
-#pragma unroll
-        for (int st = 0; st < kSteps; ++st) {
-            const float pr = mx == -INFINITY ? 0.0f : expf(s[st][j] - mx);
-            s[st][j] = pr;
-            ls += pr;
-        }
-        ls += __shfl_xor(ls, 16);
-        ls += __shfl_xor(ls, 32);
-        l[j] = ls;
-    }
-
-    float o[HPK][EPL];
-#pragma unroll
-    for (int j = 0; j < HPK; ++j)
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) o[j][e] = 0.0f;
-#pragma unroll
-    for (int st = 0; st < kSteps; ++st) {
-        const int p = wbase + st * 4 + pg;
-        const bool is_new = has_new && p == pos_new;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            const float vf = is_new ? vnew_s[dg * EPL + e] : kv_f(vraw[st].v[e]);
-#pragma unroll
-            for (int j = 0; j < HPK; ++j) o[j][e] = __builtin_fmaf(s[st][j], vf, o[j][e]);
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < HPK; ++j)
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            float v = o[j][e];
-            v += __shfl_xor(v, 16);
-            v += __shfl_xor(v, 32);
-            o[j][e] = v;
-        }
-    if (pg == 0) {
-#pragma unroll
-        for (int j = 0; j < HPK; ++j)
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) w_o[wave][j][dg * EPL + e] = o[j][e];
-    }
+        for (int e = 0; e < C::DPL; ++e) po[d0 + e] = o[e];
     if (lane == 0) {
-#pragma unroll
-        for (int j = 0; j < HPK; ++j) {
-            w_m[wave][j] = m[j];
-            w_l[wave][j] = l[j];
-        }
-    }
-    __syncthreads();
-
-    // ---- merge the 4 waves, write the chunk partial ----
-    float *po = a.part + ((size_t)g * max_chunks + c) * HPK * HD;
-    float *pml = a.part + (size_t)a.n_kv * max_chunks * HPK * HD +
-                 ((size_t)g * max_chunks + c) * HPK * 2;
-    for (int idx = tid; idx < HPK * HD; idx += kThreads) {
-        const int j = idx / HD, e = idx % HD;
-        float M = w_m[0][j];
-#pragma unroll
-        for (int w = 1; w < 4; ++w) M = fmaxf(M, w_m[w][j]);
-        float acc = 0.0f, L = 0.0f;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const float f = w_m[w][j] == -INFINITY ? 0.0f : expf(w_m[w][j] - M);
-            acc += f * w_o[w][j][e];
-            L += f * w_l[w][j];
-        }
-        po[j * HD + e] = acc;
-        if (e == 0) {
-            pml[j * 2] = M;
-            pml[j * 2 + 1] = L;
-        }
+        float *pml = a.part + (size_t)a.n_heads * max_chunks * HD + ((size_t)h * max_chunks + c) * 2;
+        pml[0] = m;
+        pml[1] = l;
     }
 }
 
+// Merge of the chunk partials: one workgroup per query head; every partial
+// load is independent and issued before the (max, sum) reduction.
 template <int HD>
-__global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict__ part, int n_kv,
-                                                        int hpk, int max_chunks, int seq_host,
-                                                        const int *__restrict__ pos_dev,
-                                                        float *__restrict__ out) {
+__global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float *__restrict__ part,
+                                                                   int n_heads, int cp,
+                                                                   int max_chunks, int seq_host,
+                                                                   const int *__restrict__ pos_dev,
+                                                                   float *__restrict__ out) {
+    constexpr int B = 32;  // chunk loads in flight per thread
+    __shared__ float w[kMaxChunkSpan / 16];
+    __shared__ float red[kMergeThreads / 64];
     const int h = blockIdx.x;
-    const int g = h / hpk, j = h % hpk;
     const int seq = pos_dev ? (*pos_dev + 1) : seq_host;
-    const int nc = (seq + kChunk - 1) / kChunk;
-    const float *po = part + (size_t)g * max_chunks * hpk * HD;
-    const float *pml = part + (size_t)n_kv * max_chunks * hpk * HD + (size_t)g * max_chunks * hpk * 2;
-    float M = -INFINITY;
-    for (int c = 0; c < nc; ++c) M = fmaxf(M, pml[(c * hpk + j) * 2]);
+    const int nc = (seq + cp - 1) / cp;
+    if (nc == 1) return;  // the chunk kernel wrote the output itself
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float *po = part + (size_t)h * max_chunks * HD;
+    const float *pml = part + (size_t)n_heads * max_chunks * HD + (size_t)h * max_chunks * 2;
+    // first batch of partial elements (thread = element e, chunk slice)
+    constexpr int EL = HD < kMergeThreads ? HD : kMergeThreads;
+    constexpr int SL = kMergeThreads / EL;  // chunk slices
+    const int e = tid % EL, sl = tid / EL;
+    float v[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+        const int cc = sl + SL * u;
+        v[u] = cc < nc ? po[(size_t)cc * HD + e] : 0.0f;
+    }
+    // (max, sum) over chunks
+    float mx = -INFINITY;
+    for (int cc = tid; cc < nc; cc += kMergeThreads) mx = fmaxf(mx, pml[cc * 2]);
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    float M = red[0];
+#pragma unroll
+    for (int i = 1; i < kMergeThreads / 64; ++i) M = fmaxf(M, red[i]);
+    __syncthreads();
+    float ls = 0.0f;
+    for (int cc = tid; cc < nc; cc += kMergeThreads) {
+        const float f = expf(pml[cc * 2] - M);
+        w[cc] = f;
+        ls += f * pml[cc * 2 + 1];
+    }
+    ls = wave_sum(ls);
+    if (lane == 0) red[wave] = ls;
+    __syncthreads();
     float L = 0.0f;
-    for (int c = 0; c < nc; ++c) L += expf(pml[(c * hpk + j) * 2] - M) * pml[(c * hpk + j) * 2 + 1];
+#pragma unroll
+    for (int i = 0; i < kMergeThreads / 64; ++i) L += red[i];
     const float inv = 1.0f / L;
-    for (int e = threadIdx.x; e < HD; e += 64) {
-        float acc = 0.0f;
-        for (int c = 0; c < nc; ++c)
-            acc += expf(pml[(c * hpk + j) * 2] - M) * po[((size_t)c * hpk + j) * HD + e];
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+        const int cc = sl + SL * u;
+        if (cc < nc) acc += w[cc] * v[u];
+    }
+    for (int cc0 = SL * B; cc0 < nc; cc0 += SL * B) {  // more than SL*B chunks
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const int cc = cc0 + sl + SL * u;
+            v[u] = cc < nc ? po[(size_t)cc * HD + e] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const int cc = cc0 + sl + SL * u;
+            if (cc < nc) acc += w[cc] * v[u];
+        }
+    }
+    if constexpr (SL > 1) {  // combine the chunk slices through LDS
+        __shared__ float part_s[kMergeThreads];
+        part_s[tid] = acc;
+        __syncthreads();
+        if (sl == 0) {
+            for (int i = 1; i < SL; ++i) acc += part_s[e + i * EL];
+            out[(size_t)h * HD + e] = acc * inv;
+        }
+    } else {
         out[(size_t)h * HD + e] = acc * inv;
     }
 }
 
-typedef void (*partial_fn)(cwi::AttnArgs, float, int);
+typedef void (*attn_fn)(cwi::AttnArgs, float, int);
 typedef void (*merge_fn)(const float *, int, int, int, int, const int *, float *);
 
+struct AttnPick {
+    attn_fn fn;
+    int threads, cp, lds;
+};
+
+template <typename KVT, int HD, int HPK>
+AttnPick make_pick() {
+    using C = Cfg<KVT, HD, HPK>;
+    return {attn_kernel<KVT, HD, HPK>, C::THREADS, C::CP, C::LDS};
+}
+
 template <typename KVT, int HD>
-partial_fn pick_hpk(int hpk) {
+AttnPick pick_hpk(int hpk) {
     switch (hpk) {
-        case 1: return attn_partial_kernel<KVT, HD, 1>;
-        case 2: return attn_partial_kernel<KVT, HD, 2>;
-        case 4: return attn_partial_kernel<KVT, HD, 4>;
-        case 8: return attn_partial_kernel<KVT, HD, 8>;
-        default: return nullptr;
+        case 1: return make_pick<KVT, HD, 1>();
+        case 2: return make_pick<KVT, HD, 2>();
+        case 4: return make_pick<KVT, HD, 4>();
+        case 8: return make_pick<KVT, HD, 8>();
+        default: return {nullptr, 0, 0, 0};
     }
 }
 
 template <typename KVT>
-partial_fn pick_hd(int hd, int hpk) {
+AttnPick pick_hd(int hd, int hpk) {
     switch (hd) {
         case 16: return pick_hpk<KVT, 16>(hpk);
         case 32: return pick_hpk<KVT, 32>(hpk);
         case 64: return pick_hpk<KVT, 64>(hpk);
         case 128: return pick_hpk<KVT, 128>(hpk);
         case 256: return pick_hpk<KVT, 256>(hpk);
-        default: return nullptr;
+        default: return {nullptr, 0, 0, 0};
     }
 }
 
@@ -319,34 +493,63 @@ merge_fn pick_merge(int hd) {
     }
 }
 
+std::mutex g_mu;
+std::map<const void *, bool> g_lds_set;
+
+int ensure_lds(attn_fn f, int lds) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const void *p = reinterpret_cast<const void *>(f);
+    if (!g_lds_set[p]) {
+        CW_HIP(hipFuncSetAttribute(p, hipFuncAttributeMaxDynamicSharedMemorySize, lds));
+        g_lds_set[p] = true;
+    }
+    return CW_OK;
+}
+
+AttnPick pick_attn(int kv_dtype, int hd, int hpk) {
+    return kv_dtype == CW_F16 ? pick_hd<_Float16>(hd, hpk) : pick_hd<float>(hd, hpk);
+}
+
 }  // namespace
 
 namespace cwi {
 
 size_t attn_scratch_floats(int n_heads, int n_kv, int hd, int max_seq) {
-    (void)n_kv;
-    const size_t chunks = (size_t)(max_seq + kChunk - 1) / kChunk;
+    const AttnPick pk = pick_attn(CW_F32, hd, n_heads / n_kv);  // f32: smallest chunk
+    const int cp = pk.cp > 0 ? pk.cp : 8;
+    const size_t chunks = (size_t)(max_seq + cp - 1) / cp;
     return chunks * (size_t)n_heads * (hd + 2);
 }
 
 int launch_attention(cw_ctx *ctx, const AttnArgs &a) {
     const int hpk = a.n_heads / a.n_kv;
-    partial_fn pf = a.kv_dtype == CW_F16 ? pick_hd<_Float16>(a.hd, hpk) : pick_hd<float>(a.hd, hpk);
+    const AttnPick pk = pick_attn(a.kv_dtype, a.hd, hpk);
     merge_fn mf = pick_merge(a.hd);
-    if (!pf || !mf) {
+    if (!pk.fn || !mf) {
         set_error("attention: unsupported head_dim=%d / heads per kv=%d", a.hd, hpk);
         return CW_ERR_ARG;
     }
-    const int max_chunks = (a.max_seq + kChunk - 1) / kChunk;
+    if (a.max_seq > kMaxChunkSpan) {
+        set_error("attention: max_seq=%d exceeds %d", a.max_seq, kMaxChunkSpan);
+        return CW_ERR_ARG;
+    }
+    CW_TRY(ensure_lds(pk.fn, pk.lds));
+    const int max_chunks = (a.max_seq + pk.cp - 1) / pk.cp;
+    if (max_chunks > kMaxChunkSpan / 16) {  // the merge kernel's weight table
+        set_error("attention: %d chunks of %d positions exceed %d", max_chunks, pk.cp,
+                  kMaxChunkSpan / 16);
+        return CW_ERR_ARG;
+    }
     const float scale = powf((float)a.hd, -0.5f);
     prof_begin(ctx, "attention");
-    hipLaunchKernelGGL(pf, dim3(max_chunks, a.n_kv), dim3(kThreads), 0, ctx->stream, a, scale,
-                       max_chunks);
+    hipLaunchKernelGGL(pk.fn, dim3(max_chunks, a.n_kv), dim3(pk.threads), pk.lds, ctx->stream, a,
+                       scale, max_chunks);
     prof_end(ctx);
-    CW_TRY(launch_check("attention_partial"));
+    CW_TRY(launch_check("attention"));
+    if (max_chunks == 1) return CW_OK;
     prof_begin(ctx, "attention_merge");
-    hipLaunchKernelGGL(mf, dim3(a.n_heads), dim3(64), 0, ctx->stream, a.part, a.n_kv, hpk,
-                       max_chunks, a.seq, a.pos_dev, a.out);
+    hipLaunchKernelGGL(mf, dim3(a.n_heads), dim3(kMergeThreads), 0, ctx->stream, a.part, a.n_heads,
+                       pk.cp, max_chunks, a.seq, a.pos_dev, a.out);
     prof_end(ctx);
     return launch_check("attention_merge");
 }
@@ -361,16 +564,17 @@ extern "C" int cw_attention(cw_ctx *ctx, const float *q, const void *k, const vo
     CW_CHECK_ARG(kv_dtype == CW_F32 || kv_dtype == CW_F16, "cw_attention: kv_dtype=%d", kv_dtype);
     CW_CHECK_ARG(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0,
                  "cw_attention: n_heads=%d n_kv_heads=%d", n_heads, n_kv_heads);
-    CW_CHECK_ARG(seq > 0, "cw_attention: seq=%d must be positive", seq);
+    CW_CHECK_ARG(seq > 0 && seq <= kMaxChunkSpan, "cw_attention: seq=%d outside [1, %d]", seq,
+                 kMaxChunkSpan);
     const int hpk = n_heads / n_kv_heads;
     CW_CHECK_ARG(hpk == 1 || hpk == 2 || hpk == 4 || hpk == 8,
                  "cw_attention: heads per kv head %d not in {1,2,4,8}", hpk);
     CW_CHECK_ARG(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128 ||
                      head_dim == 256,
                  "cw_attention: head_dim=%d not in {16,32,64,128,256}", head_dim);
+    const size_t nfl = attn_scratch_floats(n_heads, n_kv_heads, head_dim, seq);
     void *scratch = nullptr;
-    CW_TRY(ctx_scratch(ctx, attn_scratch_floats(n_heads, n_kv_heads, head_dim, seq) * sizeof(float),
-                       &scratch));
+    CW_TRY(ctx_scratch(ctx, nfl * sizeof(float), &scratch));
     AttnArgs a{};
     a.q = q;
     a.k_cache = const_cast<void *>(k);

@@ -140,8 +140,7 @@ struct AttnArgs {
     const int *pos_dev;     // device position; seq = pos+1 (fused path writes KV at pos)
     int max_seq;            // grid sizing (positions the cache can hold)
     float *out;             // [n_heads*hd]
-    float *part;            // scratch partials
-    unsigned *counters;     // [n_kv] zero-initialised, self-resetting
+    float *part;            // chunk partials, attn_scratch_floats() floats
 };
 
 size_t attn_scratch_floats(int n_heads, int n_kv, int hd, int max_seq);

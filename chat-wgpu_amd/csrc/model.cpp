@@ -276,6 +276,7 @@ int cw_model_create(cw_ctx *ctx, const cw_model_config *cfg, cw_model **out) {
     CW_CHECK_ARG(c.n_layers > 0 && c.dim > 0 && c.n_heads > 0 && c.n_kv_heads > 0 &&
                      c.hidden > 0 && c.vocab > 0 && c.max_seq > 0,
                  "cw_model_create: every dimension must be positive");
+    CW_CHECK_ARG(c.max_seq <= 32768, "cw_model_create: max_seq=%d exceeds 32768", c.max_seq);
     CW_CHECK_ARG(c.n_heads % c.n_kv_heads == 0, "cw_model_create: n_heads %% n_kv_heads != 0");
     const int hpk = c.n_heads / c.n_kv_heads;
     CW_CHECK_ARG(hpk == 1 || hpk == 2 || hpk == 4 || hpk == 8,
@@ -315,7 +316,7 @@ int cw_model_create(cw_ctx *ctx, const cw_model_config *cfg, cw_model **out) {
     }
     const size_t es = c.kv_dtype == CW_F16 ? 2 : 4;
     m->kv_layer_bytes = (size_t)c.max_seq * kv_dim * es;
-    const size_t chunks = ((size_t)c.max_seq + 127) / 128;
+    const size_t part_floats = attn_scratch_floats(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq);
     if ((rc = dalloc(m, (size_t)c.vocab * c.dim * 4, (void **)&m->embed)) ||
         (rc = dalloc(m, c.dim * 4, (void **)&m->final_norm)) ||
         (rc = alloc_q4(m, m->lm_head, c.vocab, c.dim)) ||
@@ -327,7 +328,7 @@ int cw_model_create(cw_ctx *ctx, const cw_model_config *cfg, cw_model **out) {
         (rc = dalloc(m, (size_t)q_dim * 4, (void **)&m->attn)) ||
         (rc = dalloc(m, (size_t)c.hidden * 4, (void **)&m->act)) ||
         (rc = dalloc(m, (size_t)c.vocab * 4, (void **)&m->logits)) ||
-        (rc = dalloc(m, chunks * c.n_heads * (c.head_dim + 2) * 4, (void **)&m->part)) ||
+        (rc = dalloc(m, part_floats * 4, (void **)&m->part)) ||
         (rc = dalloc(m, argmax_scratch_bytes(c.vocab), &m->argmax_scratch)) ||
         (rc = dalloc(m, sizeof(GenState), (void **)&m->state)) ||
         (rc = dalloc(m, (size_t)c.max_seq * 4, (void **)&m->prompt_dev)) ||

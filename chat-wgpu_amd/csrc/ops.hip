@@ -192,6 +192,37 @@ __global__ __launch_bounds__(kThreads) void argmax_final_kernel(const float *__r
     }
 }
 
+// HBM read probe (the examples/q4probe.rs analogue): every thread streams
+// 16-byte words over a grid-stride loop and folds them with XOR, so nothing
+// but the reads costs time; one word per workgroup is written out.
+__global__ __launch_bounds__(kThreads) void read_probe_kernel(const uint4 *__restrict__ p,
+                                                              size_t n16, uint32_t *__restrict__ out) {
+    uint4 acc = make_uint4(0, 0, 0, 0);
+    const size_t stride = (size_t)gridDim.x * kThreads;
+    size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        const uint4 a = p[i], b = p[i + stride], c = p[i + 2 * stride], d = p[i + 3 * stride];
+        acc.x ^= a.x ^ b.x ^ c.x ^ d.x;
+        acc.y ^= a.y ^ b.y ^ c.y ^ d.y;
+        acc.z ^= a.z ^ b.z ^ c.z ^ d.z;
+        acc.w ^= a.w ^ b.w ^ c.w ^ d.w;
+    }
+    for (; i < n16; i += stride) {
+        const uint4 a = p[i];
+        acc.x ^= a.x;
+        acc.y ^= a.y;
+        acc.z ^= a.z;
+        acc.w ^= a.w;
+    }
+    uint32_t v = acc.x ^ acc.y ^ acc.z ^ acc.w;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v ^= (uint32_t)__shfl_xor((int)v, off);
+    __shared__ uint32_t red[kThreads / 64];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) out[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
+}
+
 }  // namespace
 
 namespace cwi {
@@ -334,6 +365,18 @@ int cw_embed(cw_ctx *ctx, const float *table, int vocab, int dim, const uint32_t
     CW_CHECK_ARG(ctx && table && token_dev && out, "cw_embed: null argument");
     CW_CHECK_ARG(vocab > 0 && dim > 0, "cw_embed: vocab=%d dim=%d", vocab, dim);
     return launch_embed(ctx, table, vocab, dim, token_dev, out);
+}
+
+int cw_hbm_read_probe(cw_ctx *ctx, const void *buf, size_t bytes, int blocks, uint32_t *out_dev) {
+    CW_CHECK_ARG(ctx && buf && out_dev, "cw_hbm_read_probe: null argument");
+    CW_CHECK_ARG(((uintptr_t)buf & 15) == 0 && bytes >= 16,
+                 "cw_hbm_read_probe: buf must be 16-byte aligned and bytes >= 16");
+    CW_CHECK_ARG(blocks > 0 && blocks <= 65536, "cw_hbm_read_probe: blocks=%d", blocks);
+    prof_begin(ctx, "hbm_read_probe");
+    hipLaunchKernelGGL(read_probe_kernel, dim3(blocks), dim3(kThreads), 0, ctx->stream,
+                       (const uint4 *)buf, bytes / 16, out_dev);
+    prof_end(ctx);
+    return launch_check("hbm_read_probe");
 }
 
 }  // extern "C"

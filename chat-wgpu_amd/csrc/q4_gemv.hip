@@ -10,10 +10,14 @@
 //
 // Work split: a wave64 covers 64 blocks per step.  G = lanes per row (the
 // largest power of two <= 64 dividing K/32); 64/G rows share a wave step.
-// Each wave owns R row slots at a time; waves walk a persistent grid of
-// wave tiles.  The activation is staged once per workgroup into LDS as
-// [8][K/32] float4 (conflict-free: lane b reads float4 i of block b) plus the
-// per-block sums sum_j x_j.
+// A wave tile is R row slots x all K; waves walk wave tiles over a
+// persistent grid of 1024-thread workgroups (one per CU), so the activation
+// is staged into LDS once per CU: [8][K/32] float4 (conflict-free: lane b
+// reads float4 i of block b) plus the per-block sums sum_j x_j.
+//
+// Latency: every wave issues the loads of its first (tile, step) group before
+// the activation is staged, and each iteration issues the next group's loads
+// (crossing tile boundaries) before computing the current one.
 //
 // Nibble decode costs 5 VALU ops per 8 weights: AND-ing a quant dword with
 // 0x000F000F / 0x00F000F0 (and the same after one >>8) leaves two f16
@@ -37,7 +41,7 @@ namespace {
 
 using cwi::GemvArgs;
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
@@ -67,8 +71,8 @@ __device__ __forceinline__ float f16hi(uint32_t v) {
     return (float)__builtin_bit_cast(half2v, v).y;
 }
 
-// sum_j q_j * x_j over one block; xl[w] = 2^24 * x[4w..4w+3],
-// xh[w] = 2^20 * x[16+4w..16+4w+3].
+// sum_j q_j * x_j over one quant dword; xl = 2^24 * x[4w..4w+3],
+// xh = 2^20 * x[16+4w..16+4w+3].
 __device__ __forceinline__ float dot_word(uint32_t dw, float4 xl, float4 xh, float s) {
     const uint32_t a = dw & 0x000F000Fu;          // elements 4w+0, 4w+2     (q * 2^-24)
     const uint32_t b = dw & 0x00F000F0u;          // elements 16+4w+0, +2    (q * 2^-20)
@@ -86,17 +90,70 @@ __device__ __forceinline__ float dot_word(uint32_t dw, float4 xl, float4 xh, flo
     return s;
 }
 
+template <int G, int R, int EPI>
+struct Tile {
+    static constexpr int RPS = 64 / G;                         // rows per wave step
+    static constexpr int NR = (EPI == cwi::EPI_SWIGLU) ? R / 2 : R;  // distinct rows
+    static constexpr int ROWS = NR * RPS;                      // rows per wave tile
+};
+
+// Issue the loads of one (tile, block) group: R quant blocks + R scales.
+template <int G, int R, int EPI>
+__device__ __forceinline__ void load_group(const GemvArgs &a, int nb, int wt, int b, int rl,
+                                           uint4 (&qv)[R], uint32_t (&dv)[R]) {
+    using T = Tile<G, R, EPI>;
+    const int row0 = wt * T::ROWS;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        int row = row0 + (r % T::NR) * T::RPS + rl;
+        row = row < a.N ? row : a.N - 1;
+        const bool second = (EPI == cwi::EPI_SWIGLU) && r >= T::NR;
+        const uint8_t *qb = second ? a.qB : a.qA;
+        const uint16_t *sb = second ? a.sB : a.sA;
+        qv[r] = reinterpret_cast<const uint4 *>(qb)[(size_t)row * nb + b];
+        dv[r] = sb[(size_t)row * nb + b];
+    }
+}
+
 template <int G, int R, int XS, int EPI>
 __global__ __launch_bounds__(kThreads) void q4_gemv_kernel(GemvArgs a, int n_wave_tiles) {
+    using T = Tile<G, R, EPI>;
     extern __shared__ float4 lds4[];
     __shared__ float red[kWaves];
     const int K = a.K;
     const int nb = K >> 5;
     const int K4 = K >> 2;
+    const int S = nb / G;  // steps per tile
     float *sx = reinterpret_cast<float *>(lds4 + 8 * nb);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    // wave-uniform: keeps tile/row/address arithmetic in scalar registers
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int s = lane & (G - 1);
+    const int rl = lane / G;
+
+    // this wave's tiles: wv, wv + stride, ...
+    const int wv = blockIdx.x * kWaves + wave;
+    const int stride = gridDim.x * kWaves;
+    const int n_my = wv < n_wave_tiles ? (n_wave_tiles - 1 - wv) / stride + 1 : 0;
+    const int total = n_my * S;
+
+    // a ring of PD (tile, block) groups in flight per wave, issued before the
+    // activation is staged; slot u always holds group it with it % PD == u
+    constexpr int PD = R == 4 ? 2 : R == 2 ? 5 : 10;  // fits 128 VGPRs (1024-thread groups)
+    uint4 qv[PD][R];
+    uint32_t dv[PD][R];
+    int lk = 0, lstep = 0;  // next group to load
+#pragma unroll
+    for (int u = 0; u < PD; ++u) {
+        if (u < total) {
+            load_group<G, R, EPI>(a, nb, wv + lk * stride, s + lstep * G, rl, qv[u], dv[u]);
+            if (++lstep == S) {
+                lstep = 0;
+                ++lk;
+            }
+        }
+    }
 
     // ---- stage the activation (optionally RMS-normalised) ----
     float inv = 1.0f;
@@ -109,7 +166,9 @@ __global__ __launch_bounds__(kThreads) void q4_gemv_kernel(GemvArgs a, int n_wav
         ss = group_sum<64>(ss);
         if (lane == 0) red[wave] = ss;
         __syncthreads();
-        ss = (red[0] + red[1]) + (red[2] + red[3]);
+        ss = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) ss += red[w];
         inv = 1.0f / sqrtf(ss / (float)K + a.eps);
     }
     for (int idx = tid; idx < K4; idx += kThreads) {
@@ -132,93 +191,77 @@ __global__ __launch_bounds__(kThreads) void q4_gemv_kernel(GemvArgs a, int n_wav
     __syncthreads();
 
     // ---- stream the weights ----
-    constexpr int RPS = 64 / G;  // rows per wave step
-    constexpr int NR = (EPI == cwi::EPI_SWIGLU) ? R / 2 : R;  // distinct rows per slot group
-    constexpr int ROWS_PER_TILE = NR * RPS;
-    const int s = lane & (G - 1);
-    const int rl = lane / G;
-    const int N = a.N;
-
-    for (int wt = blockIdx.x * kWaves + wave; wt < n_wave_tiles; wt += gridDim.x * kWaves) {
-        const int row0 = wt * ROWS_PER_TILE;
-        const uint4 *qp[R];
-        const uint16_t *sp[R];
+    float acc[R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int rr = r % NR;
-            int row = row0 + rr * RPS + rl;
-            row = row < N ? row : N - 1;
-            const bool second = (EPI == cwi::EPI_SWIGLU) && r >= NR;
-            const uint8_t *qb = second ? a.qB : a.qA;
-            const uint16_t *sb = second ? a.sB : a.sA;
-            qp[r] = reinterpret_cast<const uint4 *>(qb) + (size_t)row * nb;
-            sp[r] = sb + (size_t)row * nb;
-        }
-        float acc[R];
-        uint4 qv[R];
-        uint32_t dv[R];
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    int k = 0, step = 0;  // group being computed
+    for (int base = 0; base < total; base += PD) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            acc[r] = 0.0f;
-            qv[r] = qp[r][s];
-            dv[r] = sp[r][s];
-        }
-        for (int b = s; b < nb; b += G) {
-            uint4 qn[R];
-            uint32_t dn[R];
-            const int bn = b + G;
-            if (bn < nb) {
+        for (int u = 0; u < PD; ++u) {
+            if (base + u < total) {
+                const int b = s + step * G;
+                float4 xv[8];
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    qn[r] = qp[r][bn];
-                    dn[r] = sp[r][bn];
-                }
-            }
-            float4 xv[8];
+                for (int i = 0; i < 8; ++i) xv[i] = lds4[i * nb + b];
+                const float sxb = sx[b];
+                // one accumulator per (row, quant dword): independent fma_mix
+                // chains interleave without dependency stalls
+                float sum[R][4];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) xv[i] = lds4[i * nb + b];
-            const float sxb = sx[b];
-            float sum[R];
+                for (int w = 0; w < 4; ++w) {
 #pragma unroll
-            for (int r = 0; r < R; ++r) sum[r] = 0.0f;
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const uint32_t dw = w == 0 ? qv[r].x : w == 1 ? qv[r].y : w == 2 ? qv[r].z : qv[r].w;
-                    sum[r] = dot_word(dw, xv[w], xv[4 + w], sum[r]);
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const float t = __builtin_fmaf(-8.0f, sxb, sum[r]);
-                const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)dv[r]);
-                acc[r] = __builtin_fmaf((float)d, t, acc[r]);
-            }
-            if (bn < nb) {
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    qv[r] = qn[r];
-                    dv[r] = dn[r];
-                }
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = group_sum<G>(acc[r]);
-        if (s == 0) {
-#pragma unroll
-            for (int rr = 0; rr < NR; ++rr) {
-                const int row = row0 + rr * RPS + rl;
-                if (row < N) {
-                    if constexpr (EPI == cwi::EPI_STORE) {
-                        a.y[row] = acc[rr];
-                    } else if constexpr (EPI == cwi::EPI_ADD) {
-                        a.y[row] = a.resid[row] + acc[rr];
-                    } else {
-                        const float g = acc[rr], u = acc[rr + NR];
-                        const float sg = g / (1.0f + expf(-g));
-                        a.y[row] = sg * u;
+                    for (int r = 0; r < R; ++r) {
+                        const uint4 q = qv[u][r];
+                        const uint32_t dw = w == 0 ? q.x : w == 1 ? q.y : w == 2 ? q.z : q.w;
+                        sum[r][w] = dot_word(dw, xv[w], xv[4 + w], 0.0f);
                     }
+                }
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const float sr = (sum[r][0] + sum[r][1]) + (sum[r][2] + sum[r][3]);
+                    const float t = __builtin_fmaf(-8.0f, sxb, sr);
+                    const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)dv[u][r]);
+                    acc[r] = __builtin_fmaf((float)d, t, acc[r]);
+                }
+                // refill this slot with the group PD ahead; past the wave's
+                // last group re-load that group (a cache hit) so the refill
+                // needs no branch
+                {
+                    const bool past = lk >= n_my;
+                    load_group<G, R, EPI>(a, nb, wv + (past ? n_my - 1 : lk) * stride,
+                                          s + (past ? S - 1 : lstep) * G, rl, qv[u], dv[u]);
+                    if (!past && ++lstep == S) {
+                        lstep = 0;
+                        ++lk;
+                    }
+                }
+                if (step == S - 1) {  // tile done: reduce over the G lanes of each row, write
+#pragma unroll
+                    for (int r = 0; r < R; ++r) acc[r] = group_sum<G>(acc[r]);
+                    if (s == 0) {
+                        const int row0 = (wv + k * stride) * T::ROWS;
+#pragma unroll
+                        for (int rr = 0; rr < T::NR; ++rr) {
+                            const int row = row0 + rr * T::RPS + rl;
+                            if (row < a.N) {
+                                if constexpr (EPI == cwi::EPI_STORE) {
+                                    a.y[row] = acc[rr];
+                                } else if constexpr (EPI == cwi::EPI_ADD) {
+                                    a.y[row] = a.resid[row] + acc[rr];
+                                } else {
+                                    const float g = acc[rr], up = acc[rr + T::NR];
+                                    const float sg = g / (1.0f + expf(-g));
+                                    a.y[row] = sg * up;
+                                }
+                            }
+                        }
+                    }
+#pragma unroll
+                    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+                }
+                if (++step == S) {
+                    step = 0;
+                    ++k;
                 }
             }
         }
@@ -232,7 +275,9 @@ gemv_fn pick_epi(int epi) {
     switch (epi) {
         case cwi::EPI_STORE: return q4_gemv_kernel<G, R, XS, cwi::EPI_STORE>;
         case cwi::EPI_ADD: return q4_gemv_kernel<G, R, XS, cwi::EPI_ADD>;
-        default: return q4_gemv_kernel<G, R, XS, cwi::EPI_SWIGLU>;
+        default:
+            if constexpr (R % 2 == 0) return q4_gemv_kernel<G, R, XS, cwi::EPI_SWIGLU>;
+            return nullptr;
     }
 }
 
@@ -244,7 +289,7 @@ gemv_fn pick_xs(int xs, int epi) {
 
 template <int G>
 gemv_fn pick_r(int r, int xs, int epi) {
-    return r == 4 ? pick_xs<G, 4>(xs, epi) : pick_xs<G, 2>(xs, epi);
+    return r == 4 ? pick_xs<G, 4>(xs, epi) : r == 2 ? pick_xs<G, 2>(xs, epi) : pick_xs<G, 1>(xs, epi);
 }
 
 gemv_fn pick(int g, int r, int xs, int epi) {
@@ -273,7 +318,11 @@ int occupancy(gemv_fn fn, int lds, int *blocks) {
     std::lock_guard<std::mutex> lk(g_occ_mu);
     const void *f = reinterpret_cast<const void *>(fn);
     if (!g_attr_set[f]) {
-        CW_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+        // static + dynamic LDS of a workgroup must fit the CU's 160 KB
+        hipFuncAttributes attr{};
+        CW_HIP(hipFuncGetAttributes(&attr, f));
+        const int max_dyn = 160 * 1024 - (int)attr.sharedSizeBytes;
+        CW_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, max_dyn));
         g_attr_set[f] = true;
     }
     OccKey k{f, lds};
@@ -311,8 +360,22 @@ int launch_q4_gemv(cw_ctx *ctx, XSrc xs, Epi epi, const GemvArgs &a) {
         const int rows = nr * rps;
         return (a.N + rows - 1) / rows;
     };
-    int r = 4;
-    if ((tiles_for(4) + kWaves - 1) / kWaves < 2 * ctx->n_cu) r = 2;
+    // R (row slots per wave tile): balance tiles over the chip's waves first
+    // (a wave with one tile more than the rest sets the kernel time), then
+    // prefer the larger R (fewer LDS reads of x per weight byte)
+    const int waves = ctx->n_cu * kWaves;
+    int r = 0;
+    double best = -1.0;
+    for (int cand : {4, 2, 1}) {
+        if (epi == EPI_SWIGLU && cand == 1) continue;
+        const int t = tiles_for(cand);
+        const int rounds = (t + waves - 1) / waves;
+        const double eff = (double)t / ((double)rounds * waves);  // mean / max tiles per wave
+        if (eff > best + 0.05) {
+            best = eff;
+            r = cand;
+        }
+    }
     const int n_tiles = tiles_for(r);
     gemv_fn fn = pick(g, r, xs, epi);
     const int lds = nb * 132;

@@ -69,6 +69,7 @@ _SIGS = {
     "cw_argmax": (_I, [_P, _P, _I, _P]),
     "cw_kv_write": (_I, [_P, _P, _P, _I, _I, _I, _P, _P]),
     "cw_embed": (_I, [_P, _P, _I, _I, _P, _P]),
+    "cw_hbm_read_probe": (_I, [_P, _P, _SZ, _I, _P]),
     "cw_q4_quantize": (_I, [_P, _SZ, _SZ, _P, _P]),
     "cw_q4_split_blocks": (_I, [_P, _SZ, _P, _P]),
     "cw_synth_key": (_U64, [_U64, C.c_char_p]),
@@ -311,6 +312,9 @@ class Context:
         o = self.empty(dim)
         check(lib().cw_embed(self.h, table.ptr, vocab, dim, token_dev.ptr, o.ptr))
         return o
+
+    def hbm_read_probe(self, buf, nbytes, blocks, out):
+        check(lib().cw_hbm_read_probe(self.h, buf.ptr, nbytes, blocks, out.ptr))
 
 
 # ---------------------------------------------------------------- model

@@ -121,6 +121,11 @@ int cw_kv_write(cw_ctx *ctx, void *k_cache, void *v_cache, int kv_dtype, int pos
 int cw_embed(cw_ctx *ctx, const float *table, int vocab, int dim, const uint32_t *token_dev,
              float *out);
 
+/* examples/q4probe.rs (raw read-bandwidth sweep): stream `bytes` of buf with
+ * 128-bit loads over `blocks` workgroups of 256 threads, XOR-fold, write one
+ * word per workgroup to out_dev.  Time it with the profiler or events. */
+int cw_hbm_read_probe(cw_ctx *ctx, const void *buf, size_t bytes, int blocks, uint32_t *out_dev);
+
 /* ---------------------------------------------------------------- */
 /* Host-side Q4 helpers                                              */
 /* ---------------------------------------------------------------- */

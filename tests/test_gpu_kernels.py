@@ -99,11 +99,17 @@ def test_q4_unpack_positions_wide_rows(ctx):
 
 
 def test_q4_gemv_all_eights_is_zero(ctx):
+    """All nibbles 8 (the q4bench input 0x88888888): the weights are exactly
+    zero.  Like the reference shader (q4.wgsl:131, s_total = (s_lo + s_hi) -
+    8 * x_sum) the kernel factors the -8 out of the block sum, so the result
+    is zero up to f32 cancellation: |y| <= 1e-6 * sum_b |d_b| * 8 * sum|x_b|."""
     in_f, out_f = 1024, 3072
     s, _, x = synth_gemv(out_f, in_f, 3)
     q = np.full((out_f, in_f // 32, 16), 0x88, np.uint8)
     y = ctx.q4_gemv(ctx.storage(x), ctx.storage(s), ctx.storage(q), in_f, out_f).download()
-    assert np.all(y == 0.0)
+    d = s.view(np.float16).astype(np.float64)
+    cond = (d * 8 * np.abs(x.astype(np.float64)).reshape(-1, 32).sum(1)).sum(1)
+    assert np.all(np.abs(y) <= 1e-6 * cond)
 
 
 @pytest.mark.parametrize("in_f,out_f", [(2048, 1024), (12288, 4096), (96, 70)])
