@@ -6,9 +6,10 @@ weights of seeded synthetic values, tied Q4 LM head, f16 KV cache pre-filled
 with 4096 positions of N(0,1), batch 1.  Timed: K decode steps from position
 4096 (HIP-graph replay of the device-resident step), inputs resident in HBM.
 
-Prints one JSON line.  Extra fields: the Q4 GEMV roofline (HIP events on the
-library stream over profiled decode steps), the CPU oracle baseline on a
-bounded sample, and the Qwen3-0.6B-shape token loop.
+Prints one JSON line.  Extra fields: the roofline of the dominant kernel
+family, the Q4 GEMV (HIP events on the library stream around every launch of
+8 eager steps of the same workload), the whole-token byte roofline, the CPU
+oracle baseline on a bounded sample, and the Qwen3-0.6B-shape token loop.
 
   python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -38,33 +39,6 @@ def q4_bytes(out_f, in_f):
     return out_f * (in_f // 32) * 18
 
 
-def gemv_bytes_per_token(cfg):
-    """Algorithmic bytes of one token's Q4 GEMV launches: weights (18 B per 32)
-    + activation read (K f32) + output write (N f32) per launch."""
-    q, kv, d, h, v = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim, cfg.dim, \
-        cfg.hidden, cfg.vocab
-    per_layer = [
-        (q + 2 * kv, d, 1),  # fused RMSNorm + QKV
-        (d, q, 2),           # O + residual (reads residual too)
-        (2 * h, d, 0),       # gate/up pair (+SwiGLU): 2h rows, writes h
-        (d, h, 2),           # down + residual
-    ]
-    total = 0
-    for n, k, extra in per_layer:
-        w = q4_bytes(n, k)
-        out_n = h if n == 2 * h else n
-        total += w + 4 * k + 4 * out_n + (4 * n if extra == 2 else 0)
-    total *= cfg.n_layers
-    total += q4_bytes(v, d) + 4 * d + 4 * v
-    weights = cfg.n_layers * (q4_bytes(q + 2 * kv, d) + q4_bytes(d, q) + q4_bytes(2 * h, d) +
-                              q4_bytes(d, h)) + q4_bytes(v, d)
-    return total, weights
-
-
-def kv_bytes_per_token(cfg, seq, es):
-    return cfg.n_layers * seq * cfg.n_kv_heads * cfg.head_dim * 2 * es
-
-
 def cpu_info():
     model = platform.processor() or ""
     try:
@@ -77,12 +51,34 @@ def cpu_info():
     return model, os.cpu_count()
 
 
-def profile_gemv(ctx, model, n_steps):
-    """Per-kernel HIP-event timings over n_steps eager decode steps."""
-    ctx.profile_begin()
-    model.decode_async(n_steps, use_graph=False)
-    rows = ctx.profile_report()
-    return {name: (count / n_steps, ms / n_steps) for name, count, ms in rows}
+def gemv_bytes_per_token(cfg):
+    """Algorithmic HBM bytes of one token's Q4 GEMV launches: each weight once
+    (18 B per 32), the activation read (K f32) and the output write (N f32),
+    plus the residual read of the O and down launches."""
+    q, kv, d, h, v = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim, cfg.dim, \
+        cfg.hidden, cfg.vocab
+    per_layer = [  # (rows, K, output floats, residual floats)
+        (q + 2 * kv, d, q + 2 * kv, 0),  # RMSNorm + q|k|v
+        (d, q, d, d),                    # O + residual
+        (2 * h, d, h, 0),                # gate|up + SwiGLU
+        (d, h, d, d),                    # down + residual
+    ]
+    total = sum(q4_bytes(n, k) + 4 * k + 4 * o + 4 * r for n, k, o, r in per_layer)
+    total = total * cfg.n_layers + q4_bytes(v, d) + 4 * d + 4 * v
+    return total
+
+
+def step_bytes(cfg, seq, es):
+    """Algorithmic HBM bytes of one decode step at sequence length seq: every
+    Q4 weight once (18 B per 32), the K and V rows of seq positions read and
+    one row of each written, the embedding row, the norm gains, the logits."""
+    q, kv = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+    d, h, v, L = cfg.dim, cfg.hidden, cfg.vocab, cfg.n_layers
+    w = L * (q4_bytes(q + 2 * kv, d) + q4_bytes(d, q) + q4_bytes(2 * h, d) + q4_bytes(d, h))
+    w += q4_bytes(v, d)
+    kv_rw = L * (seq + 1) * kv * 2 * es
+    small = 4 * d + 4 * (L * (2 * d + 2 * cfg.head_dim) + d) + 4 * v
+    return w + kv_rw + small, w
 
 
 def cpu_baseline_8b(cfg, weights, k, v, start_tok, budget_s):
@@ -113,9 +109,9 @@ def bench_06b(ctx, warm=True):
     m.finalize()
     prompt = cw.synth_tokens(cw.synth_key(2024, "prompt"), P, cfg.vocab)
     if warm:
-        m.generate(prompt, N, use_graph=True)
+        m.generate(prompt, N, mode=cw.STEP_GRAPH)
     t0 = time.perf_counter()
-    m.generate(prompt, N, use_graph=True)
+    m.generate(prompt, N, mode=cw.STEP_GRAPH)
     el = time.perf_counter() - t0
     m.close()
     return (P + N - 1) / el, el
@@ -139,7 +135,7 @@ def main():
     ctx = cw.Context(0)
     info = ctx.info()
     log(f"device {info}")
-    cfg = cw.make_config(36, 4096, 32, 8, 128, 12288, 151936, PRE + max(K, W), cw.CW_F16,
+    cfg = cw.make_config(36, 4096, 32, 8, 128, 12288, 151936, PRE + max(K, W, 8) + 1, cw.CW_F16,
                          1e-6, 1e6)
     t = time.perf_counter()
     weights = cw.synthetic_weights(cfg, 8008)
@@ -155,29 +151,38 @@ def main():
     log(f"model ready in {time.perf_counter() - t:.1f}s")
 
     m.reset_state(start, PRE)
-    m.decode_async(W, use_graph=True)
+    m.decode_async(W, mode=cw.STEP_GRAPH)
     ctx.flush()
     log("warmup done")
 
+    # timed: K decode steps from position PRE, the step replayed as a HIP graph
     m.reset_state(start, PRE)
     ctx.flush()
     t0 = time.perf_counter()
-    m.decode_async(K, use_graph=True)
+    m.decode_async(K, mode=cw.STEP_GRAPH)
     ctx.flush()
     el = time.perf_counter() - t0
     toks = m.tokens(K)
     tok_s = K / el
     log(f"timed {K} steps in {el * 1e3:.2f} ms -> {tok_s:.1f} tok/s; first tokens {toks[:8]}")
 
-    # roofline of the dominant kernel family (Q4 GEMV) over profiled eager steps
+    # roofline of the dominant kernel family (the Q4 GEMVs): HIP events on the
+    # library stream around every launch of NP eager steps of the same workload
+    NP = 8
     m.reset_state(start, PRE)
-    prof = profile_gemv(ctx, m, 8)
-    gemv_ms = sum(ms for name, (_, ms) in prof.items() if name.startswith("q4_gemv"))
-    gemv_launches = sum(c for name, (c, _) in prof.items() if name.startswith("q4_gemv"))
-    gbytes, wbytes = gemv_bytes_per_token(cfg)
+    ctx.flush()
+    ctx.profile_begin()
+    m.decode_async(NP, mode=cw.STEP_EAGER)
+    prof = {name: (count / NP, ms / NP) for name, count, ms in ctx.profile_report()}
+    gemv = {n: v for n, v in prof.items() if n.startswith("q4_gemv")}
+    gemv_ms = sum(ms for _, ms in gemv.values())
+    gemv_launches = sum(c for c, _ in gemv.values())
+    gbytes = gemv_bytes_per_token(cfg)
     achieved = gbytes / (gemv_ms * 1e-3) / 1e9
-    kernel_ms = sum(ms for _, (_, ms) in prof.items())
-    log("per-token kernel ms: " + ", ".join(f"{n}={ms:.3f}" for n, (_, ms) in prof.items()))
+    kernel_ms = sum(ms for _, ms in prof.values())
+    log("per-token kernel ms (eager, events): " +
+        ", ".join(f"{n}={ms:.3f}" for n, (_, ms) in prof.items()))
+    bytes_avg = sum(step_bytes(cfg, PRE + i + 1, 2)[0] for i in range(K)) / K
 
     result = {
         "metric": "decode tokens/s (Qwen3-0.6B/8B Q4_0, 1 GPU); Q4 GEMV HBM GB/s vs peak",
@@ -193,22 +198,24 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded Q4_0 weights, N(0,1) f16 KV pre-fill)",
         "config": {"workload": "qwen3-8b-shape q4_0 greedy decode, batch 1, KV 4096->"
-                               f"{PRE + K} f16, {K} steps, hipGraph step replay",
+                               f"{PRE + K} f16, {K} steps, step replayed as a HIP graph",
                    "weights": "q4_0", "hidden": 4096, "layers": 36, "heads": "32/8x128",
                    "intermediate": 12288, "vocab": 151936, "kv_prefill": PRE,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": None,
-                     "kernel": "q4_gemv* (all Q4 GEMV launches of one token)",
+                     "kernel": "q4_gemv_kernel (all 4 fused variants; 4 launches per layer "
+                               "+ the LM head)",
                      "algorithmic_bytes_per_token": gbytes,
-                     "gemv_ms_per_token": round(gemv_ms, 4),
-                     "gemv_launches_per_token": gemv_launches},
-        "token_roofline": {
-            "bytes_per_token": wbytes + kv_bytes_per_token(cfg, PRE + K // 2, 2),
-            "ideal_ms": round((wbytes + kv_bytes_per_token(cfg, PRE + K // 2, 2)) /
-                              (HBM_PEAK_GBS * 1e6), 4),
-            "kernel_ms_per_token": round(kernel_ms, 4)},
+                     "avg_bytes_per_launch": round(gbytes / gemv_launches),
+                     "avg_launch_us": round(gemv_ms * 1e3 / gemv_launches, 2),
+                     "launches_per_token": gemv_launches},
+        "token_roofline": {"algorithmic_bytes_per_token": round(bytes_avg),
+                           "ideal_ms_at_peak": round(bytes_avg / (HBM_PEAK_GBS * 1e6), 4),
+                           "kernel_ms_per_token_eager": round(kernel_ms, 4),
+                           "frac_of_peak": round(bytes_avg / (el / K) / 1e9 / HBM_PEAK_GBS, 4)},
+        "extras": {},
     }
 
     if not args.no_cpu_baseline:
@@ -225,9 +232,9 @@ def main():
 
     if not args.no_extras:
         tps06, el06 = bench_06b(ctx)
-        result["extras"] = {"qwen3_0.6b_token_loop_tok_s": round(tps06, 1),
-                            "qwen3_0.6b_token_loop": "32 prompt + 128 greedy, f32 KV, "
-                                                     "159 forwards incl. prompt"}
+        result["extras"]["qwen3_0.6b_token_loop_tok_s"] = round(tps06, 1)
+        result["extras"]["qwen3_0.6b_token_loop"] = ("32 prompt + 128 greedy, f32 KV, 159 "
+                                                     "forwards incl. prompt, HIP graph")
     ctx.close()
     print(json.dumps(result), flush=True)
 

@@ -171,4 +171,56 @@ size_t argmax_scratch_bytes(int n);
 int launch_argmax(cw_ctx *ctx, const float *logits, int n, uint32_t *out_dev, void *scratch,
                   GenState *state, const uint32_t *prompt_dev, uint32_t *tokens_out_dev);
 
+// ---- the fused decode step (one persistent cooperative kernel per token)
+
+constexpr int kStepMaxKv = 32;
+
+struct StepLayer {
+    const float *attn_norm, *q_norm, *k_norm, *ffn_norm;
+    const uint8_t *qkv_q;
+    const uint16_t *qkv_s;
+    const uint8_t *o_q;
+    const uint16_t *o_s;
+    const uint8_t *gu_q;      // gate rows then up rows: [2*hidden][dim]
+    const uint16_t *gu_s;
+    const uint8_t *down_q;
+    const uint16_t *down_s;
+    void *kc, *vc;  // this layer's [max_seq][n_kv*128] caches
+};
+
+struct StepArgs {
+    const StepLayer *layers;  // device array [n_layers]
+    int n_layers, dim, n_heads, n_kv, hidden, vocab;
+    int max_chunks;           // attention partial slots per head
+    int max_seq;              // KV cache capacity (positions)
+    float eps, scale;
+    const float *embed, *final_norm;
+    const uint8_t *lm_q;
+    const uint16_t *lm_s;
+    const float *cos_t, *sin_t;
+    // per-launch activations, each written once: h_a [L+1][dim], h_b [L][dim],
+    // qkv [L][q+2kv], attn [L][q], act [L][2*hidden] (gate then up outputs)
+    float *h_a, *h_b, *qkv, *attn, *act;
+    float *part;              // [n_heads][max_chunks][130]
+    float *logits, *hidden_out;
+    float *am_v;              // per-workgroup argmax [n_cu]
+    uint32_t *am_i;
+    unsigned *sync;           // step_sync_words() counters, zero between launches
+    GenState *state;
+    const uint32_t *prompt;
+    uint32_t *tokens, *argmax_out;
+    long long timeout;        // barrier spin limit in wall-clock ticks
+    long long *trace;         // optional phase stamps (workgroup 0), else null
+};
+
+size_t step_sync_words();
+int step_sync_err_index();
+int step_cpmax(int kv_dtype, int hpk);
+int step_lds_bytes(int kv_dtype, int hpk, int max_seq);
+// nullptr if the fused step supports the shape, else the reason
+const char *step_unsupported(int head_dim, int hpk, int n_kv, int dim, int q_dim, int hidden,
+                             int max_seq);
+// a_dev: the argument block in device memory
+int launch_decode_step(cw_ctx *ctx, const StepArgs *a_dev, int kv_dtype, int hpk, int max_seq);
+
 }  // namespace cwi

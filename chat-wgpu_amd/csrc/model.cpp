@@ -34,6 +34,7 @@ struct Q4W {
 
 struct Layer {
     float *attn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *ffn_norm = nullptr;
+    // q|k|v rows in one matrix
     Q4W qkv, wo, gate, up, down;
 };
 
@@ -67,9 +68,21 @@ struct cw_model {
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
     std::vector<void *> allocs;
+
+    // fused decode step (one persistent kernel per token)
+    const char *fused_unsupported = nullptr;
+    StepArgs step{};
+    StepArgs *step_dev = nullptr;  // `step` in device memory (the kernel reads it there)
+    StepLayer *step_layers = nullptr;
+    unsigned *step_sync = nullptr;
 };
 
 namespace {
+
+// The persistent decode-step kernel is switched off until the illegal memory
+// access its last GPU run raised is explained; every entry point that would
+// launch it returns CW_ERR_STATE instead.
+constexpr bool kFusedStepDisabled = true;
 
 int dalloc(cw_model *m, size_t bytes, void **out) {
     void *p = nullptr;
@@ -237,13 +250,123 @@ int ensure_graph(cw_model *m) {
     return CW_OK;
 }
 
-int run_steps(cw_model *m, int n, int use_graph) {
-    if (use_graph) {
+// The fused step's counters after a launch sequence: a set error word means
+// a grid barrier timed out; the counters are cleared for the next launch.
+int check_fused(cw_model *m) {
+    if (!m->step_sync) return CW_OK;
+    unsigned err = 0;
+    CW_HIP(hipMemcpyAsync(&err, m->step_sync + step_sync_err_index(), 4, hipMemcpyDeviceToHost,
+                          m->ctx->stream));
+    CW_HIP(hipStreamSynchronize(m->ctx->stream));
+    if (err) {
+        CW_HIP(hipMemset(m->step_sync, 0, step_sync_words() * 4));
+        set_error(err == 2 ? "decode step: position outside the KV cache (launch skipped)"
+                           : "decode step: a grid barrier timed out (launch abandoned)");
+        return CW_ERR_HIP;
+    }
+    return CW_OK;
+}
+
+int run_steps(cw_model *m, int n, int mode) {
+    if (mode == CW_STEP_FUSED) {
+        if (kFusedStepDisabled) {
+            set_error("fused decode step disabled: its last GPU run raised an illegal memory "
+                      "access whose cause is not yet found (use CW_STEP_GRAPH)");
+            return CW_ERR_STATE;
+        }
+        if (m->fused_unsupported) {
+            set_error("fused decode step unavailable for this model: %s", m->fused_unsupported);
+            return CW_ERR_ARG;
+        }
+        const auto &c = m->cfg;
+        for (int i = 0; i < n; ++i)
+            CW_TRY(launch_decode_step(m->ctx, m->step_dev, c.kv_dtype, c.n_heads / c.n_kv_heads,
+                                      c.max_seq));
+    } else if (mode == CW_STEP_GRAPH) {
         CW_TRY(ensure_graph(m));
         for (int i = 0; i < n; ++i) CW_HIP(hipGraphLaunch(m->graph_exec, m->ctx->stream));
-    } else {
+    } else if (mode == CW_STEP_EAGER) {
         for (int i = 0; i < n; ++i) CW_TRY(enqueue_step(m));
+    } else {
+        set_error("unknown step mode %d", mode);
+        return CW_ERR_ARG;
     }
+    return CW_OK;
+}
+
+// Buffers and the layer table of the fused step (after every weight exists).
+int setup_fused(cw_model *m) {
+    const auto &c = m->cfg;
+    m->fused_unsupported = step_unsupported(c.head_dim, c.n_heads / c.n_kv_heads, c.n_kv_heads,
+                                            c.dim, m->q_dim, c.hidden, c.max_seq);
+    if (m->fused_unsupported) return CW_OK;
+    const int L = c.n_layers;
+    std::vector<StepLayer> host(L);
+    for (int i = 0; i < L; ++i) {
+        const Layer &y = m->layers[i];
+        StepLayer &s = host[i];
+        s.attn_norm = y.attn_norm;
+        s.q_norm = y.q_norm;
+        s.k_norm = y.k_norm;
+        s.ffn_norm = y.ffn_norm;
+        s.qkv_q = y.qkv.q;
+        s.qkv_s = y.qkv.s;
+        s.o_q = y.wo.q;
+        s.o_s = y.wo.s;
+        // the fused step reads gate|up as one [2*hidden][dim] matrix; the
+        // separate allocations below are not that layout (the step is off)
+        s.gu_q = y.gate.q;
+        s.gu_s = y.gate.s;
+        s.down_q = y.down.q;
+        s.down_s = y.down.s;
+        s.kc = (char *)m->kcache + (size_t)i * m->kv_layer_bytes;
+        s.vc = (char *)m->vcache + (size_t)i * m->kv_layer_bytes;
+    }
+    StepArgs &a = m->step;
+    CW_TRY(dalloc(m, sizeof(StepLayer) * L, (void **)&m->step_layers));
+    CW_HIP(hipMemcpy(m->step_layers, host.data(), sizeof(StepLayer) * L, hipMemcpyHostToDevice));
+    const int max_chunks = (c.max_seq + 7) / 8;
+    CW_TRY(dalloc(m, (size_t)(L + 1) * c.dim * 4, (void **)&a.h_a));
+    CW_TRY(dalloc(m, (size_t)L * c.dim * 4, (void **)&a.h_b));
+    CW_TRY(dalloc(m, (size_t)L * (m->q_dim + 2 * m->kv_dim) * 4, (void **)&a.qkv));
+    CW_TRY(dalloc(m, (size_t)L * m->q_dim * 4, (void **)&a.attn));
+    CW_TRY(dalloc(m, (size_t)L * 2 * c.hidden * 4, (void **)&a.act));
+    CW_TRY(dalloc(m, (size_t)c.n_heads * max_chunks * (c.head_dim + 2) * 4, (void **)&a.part));
+    CW_TRY(dalloc(m, (size_t)m->ctx->n_cu * 4, (void **)&a.am_v));
+    CW_TRY(dalloc(m, (size_t)m->ctx->n_cu * 4, (void **)&a.am_i));
+    CW_TRY(dalloc(m, step_sync_words() * 4, (void **)&m->step_sync));
+    CW_HIP(hipMemset(m->step_sync, 0, step_sync_words() * 4));
+    int rate_khz = 0;
+    CW_HIP(hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, m->ctx->device));
+    if (rate_khz <= 0) rate_khz = 100000;
+    a.layers = m->step_layers;
+    a.n_layers = L;
+    a.dim = c.dim;
+    a.n_heads = c.n_heads;
+    a.n_kv = c.n_kv_heads;
+    a.hidden = c.hidden;
+    a.vocab = c.vocab;
+    a.max_chunks = max_chunks;
+    a.max_seq = c.max_seq;
+    a.eps = c.eps;
+    a.scale = powf((float)c.head_dim, -0.5f);
+    a.embed = m->embed;
+    a.final_norm = m->final_norm;
+    a.lm_q = m->lm_head.q;
+    a.lm_s = m->lm_head.s;
+    a.cos_t = m->cos_t;
+    a.sin_t = m->sin_t;
+    a.logits = m->logits;
+    a.hidden_out = m->hidden_out;
+    a.sync = m->step_sync;
+    a.state = m->state;
+    a.prompt = m->prompt_dev;
+    a.tokens = m->tokens_dev;
+    a.argmax_out = m->argmax_out;
+    a.timeout = (long long)rate_khz * 1000 * 2;  // 2 s
+    a.trace = nullptr;
+    CW_TRY(dalloc(m, sizeof(StepArgs), (void **)&m->step_dev));
+    CW_HIP(hipMemcpy(m->step_dev, &a, sizeof(StepArgs), hipMemcpyHostToDevice));
     return CW_OK;
 }
 
@@ -477,6 +600,7 @@ int cw_model_finalize(cw_model *m) {
         CW_TRY(cw_q4_quantize(e.data(), c.vocab, c.dim, s.data(), q.data()));
         CW_TRY(upload_rows(m, m->lm_head, 0, c.vocab, s.data(), q.data()));
     }
+    if (!m->step_layers) CW_TRY(setup_fused(m));
     m->finalized = true;
     return CW_OK;
 }
@@ -526,7 +650,7 @@ int cw_model_hidden(cw_model *m, float *host_out) {
 }
 
 int cw_generate(cw_model *m, const uint32_t *prompt, int n_prompt, int max_new, int start_pos,
-                int use_graph, uint32_t *out_tokens) {
+                int mode, uint32_t *out_tokens) {
     CW_CHECK_ARG(m && prompt && out_tokens, "cw_generate: null argument");
     CW_TRY(require_final(m, "cw_generate"));
     CW_CHECK_ARG(n_prompt >= 1 && max_new >= 1, "cw_generate: n_prompt=%d max_new=%d", n_prompt,
@@ -541,11 +665,11 @@ int cw_generate(cw_model *m, const uint32_t *prompt, int n_prompt, int max_new, 
     CW_HIP(hipMemcpy(m->prompt_dev, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice));
     GenState s{start_pos, prompt[0], start_pos, n_prompt, 0, max_new};
     CW_TRY(set_state(m, s));
-    CW_TRY(run_steps(m, (int)total, use_graph));
+    CW_TRY(run_steps(m, (int)total, mode));
     CW_HIP(hipMemcpyAsync(out_tokens, m->tokens_dev, (size_t)max_new * 4, hipMemcpyDeviceToHost,
                           m->ctx->stream));
     CW_HIP(hipStreamSynchronize(m->ctx->stream));
-    return CW_OK;
+    return check_fused(m);
 }
 
 int cw_model_reset_state(cw_model *m, uint32_t token, int pos) {
@@ -556,7 +680,7 @@ int cw_model_reset_state(cw_model *m, uint32_t token, int pos) {
     return set_state(m, s);
 }
 
-int cw_model_decode_async(cw_model *m, int n_steps, int use_graph) {
+int cw_model_decode_async(cw_model *m, int n_steps, int mode) {
     CW_CHECK_ARG(m != nullptr && n_steps >= 0, "cw_model_decode_async: bad argument");
     CW_TRY(require_final(m, "cw_model_decode_async"));
     GenState s{};
@@ -565,11 +689,59 @@ int cw_model_decode_async(cw_model *m, int n_steps, int use_graph) {
     CW_CHECK_ARG(s.pos + n_steps <= m->cfg.max_seq,
                  "cw_model_decode_async: %d steps from pos %d exceed max_seq %d", n_steps, s.pos,
                  m->cfg.max_seq);
-    return run_steps(m, n_steps, use_graph);
+    return run_steps(m, n_steps, mode);
+}
+
+int cw_model_profile_step(cw_model *m, int64_t *ticks, int max_n, int *n_out, double *tick_hz) {
+    CW_CHECK_ARG(m && ticks && n_out && tick_hz, "cw_model_profile_step: null argument");
+    CW_TRY(require_final(m, "cw_model_profile_step"));
+    if (kFusedStepDisabled) {
+        set_error("fused decode step disabled (see CW_STEP_FUSED)");
+        return CW_ERR_STATE;
+    }
+    if (m->fused_unsupported) {
+        set_error("fused decode step unavailable for this model: %s", m->fused_unsupported);
+        return CW_ERR_ARG;
+    }
+    GenState s{};
+    CW_HIP(hipMemcpyAsync(&s, m->state, sizeof s, hipMemcpyDeviceToHost, m->ctx->stream));
+    CW_HIP(hipStreamSynchronize(m->ctx->stream));
+    CW_CHECK_ARG(s.pos < m->cfg.max_seq, "cw_model_profile_step: pos %d at max_seq", s.pos);
+    const int n = 20 * m->cfg.n_layers + 8;  // stamps written by one launch
+    long long *dev = nullptr;
+    StepArgs *args_dev = nullptr;
+    CW_HIP(hipMalloc(&dev, (size_t)n * 8 + sizeof(StepArgs)));
+    args_dev = reinterpret_cast<StepArgs *>(dev + n);
+    StepArgs a = m->step;
+    a.trace = dev;
+    hipError_t e = hipMemsetAsync(dev, 0, (size_t)n * 8, m->ctx->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(args_dev, &a, sizeof a, hipMemcpyHostToDevice, m->ctx->stream);
+    const auto &c = m->cfg;
+    int rc = e == hipSuccess ? CW_OK : hip_fail(e, "trace setup", __FILE__, __LINE__);
+    if (rc == CW_OK)
+        rc = launch_decode_step(m->ctx, args_dev, c.kv_dtype, c.n_heads / c.n_kv_heads, c.max_seq);
+    std::vector<long long> host(n);
+    if (rc == CW_OK) {
+        e = hipMemcpyAsync(host.data(), dev, (size_t)n * 8, hipMemcpyDeviceToHost, m->ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(m->ctx->stream);
+        if (e != hipSuccess) rc = hip_fail(e, "trace download", __FILE__, __LINE__);
+    }
+    hipFree(dev);
+    CW_TRY(rc);
+    CW_TRY(check_fused(m));
+    const int k = n < max_n ? n : max_n;
+    for (int i = 0; i < k; ++i) ticks[i] = host[i];
+    *n_out = k;
+    int rate_khz = 0;
+    CW_HIP(hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, m->ctx->device));
+    *tick_hz = (double)rate_khz * 1000.0;
+    return CW_OK;
 }
 
 int cw_model_tokens(cw_model *m, uint32_t *host_out, int max_n, int *n_out) {
     CW_CHECK_ARG(m && host_out && n_out, "cw_model_tokens: null argument");
+    CW_TRY(check_fused(m));
     GenState s{};
     CW_HIP(hipMemcpyAsync(&s, m->state, sizeof s, hipMemcpyDeviceToHost, m->ctx->stream));
     CW_HIP(hipStreamSynchronize(m->ctx->stream));

@@ -17,6 +17,10 @@ LIB_PATH = os.path.join(_PKG, "libchatwgpu.so")
 CW_F32 = 0
 CW_F16 = 1
 
+STEP_EAGER = 0   # one launch per op
+STEP_GRAPH = 1   # the op launches of one step replayed as a HIP graph
+STEP_FUSED = 2   # one persistent cooperative kernel per step
+
 _P = C.c_void_p
 _I = C.c_int
 _SZ = C.c_size_t
@@ -91,6 +95,7 @@ _SIGS = {
     "cw_model_decode_async": (_I, [_P, _I, _I]),
     "cw_model_reset_state": (_I, [_P, _U32, _I]),
     "cw_model_tokens": (_I, [_P, _P, _I, C.POINTER(_I)]),
+    "cw_model_profile_step": (_I, [_P, _P, _I, C.POINTER(_I), C.POINTER(C.c_double)]),
     "cw_profile_begin": (_I, [_P]),
     "cw_profile_report": (_I, [_P, C.c_char_p, _SZ]),
 }
@@ -409,18 +414,34 @@ class Model:
         check(lib().cw_model_hidden(self.h, _ptr(out)))
         return out
 
-    def generate(self, prompt, max_new, start_pos=0, use_graph=True):
+    def generate(self, prompt, max_new, start_pos=0, mode=STEP_GRAPH):
         prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
         out = np.empty(max_new, np.uint32)
         check(lib().cw_generate(self.h, _ptr(prompt), len(prompt), max_new, start_pos,
-                                int(use_graph), _ptr(out)))
+                                int(mode), _ptr(out)))
         return out
 
     def reset_state(self, token, pos):
         check(lib().cw_model_reset_state(self.h, int(token), int(pos)))
 
-    def decode_async(self, n_steps, use_graph=True):
-        check(lib().cw_model_decode_async(self.h, n_steps, int(use_graph)))
+    def decode_async(self, n_steps, mode=STEP_GRAPH):
+        check(lib().cw_model_decode_async(self.h, n_steps, int(mode)))
+
+    def profile_step(self):
+        """One fused step with phase stamps, in microseconds from its start:
+        (list of (barrier arrive, release) pairs, end of LM head, array
+        [layer][phase][after staging, after compute]; 0 where not stamped)."""
+        L = self.cfg.n_layers
+        n_max = 20 * L + 8
+        buf = np.zeros(n_max, np.int64)
+        n = _I()
+        hz = C.c_double()
+        check(lib().cw_model_profile_step(self.h, _ptr(buf), n_max, C.byref(n), C.byref(hz)))
+        us = np.where(buf > 0, (buf - buf[0]) / hz.value * 1e6, 0.0)
+        nb = 5 * L
+        pairs = [(us[2 * e], us[2 * e + 1]) for e in range(1, nb + 1)]
+        sub = us[10 * L + 4:10 * L + 4 + 10 * L].reshape(L, 5, 2)
+        return pairs, us[10 * L + 2], sub
 
     def tokens(self, max_n):
         out = np.empty(max_n, np.uint32)

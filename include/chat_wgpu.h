@@ -203,16 +203,30 @@ int cw_model_step(cw_model *m, uint32_t token, int pos, uint32_t *argmax_out);
 int cw_model_logits(cw_model *m, float *host_out);
 /* Download the final hidden state [dim] (post final norm) of the last step. */
 int cw_model_hidden(cw_model *m, float *host_out);
+/* How a decode step is executed (cw_generate, cw_model_decode_async). */
+#define CW_STEP_EAGER 0  /* 2 + 6*n_layers kernel launches per token */
+#define CW_STEP_GRAPH 1  /* the same launches captured once as a HIP graph and replayed */
+#define CW_STEP_FUSED 2  /* one persistent cooperative kernel per token (head_dim 128) */
+
 /* model::generate (src/model/mod.rs:57-125): greedy loop over the prompt then
  * max_new produced tokens (P+N-1 forwards), the whole step device-resident
- * (position and token live on the device) and replayed as a HIP graph when
- * use_graph != 0.  The first prompt token is fed at start_pos (0 = empty
- * cache).  Writes max_new ids to out_tokens. */
+ * (position and token live on the device), executed as `mode` (CW_STEP_*).
+ * The first prompt token is fed at start_pos (0 = empty cache).  Writes
+ * max_new ids to out_tokens.  CW_STEP_FUSED returns CW_ERR_ARG for shapes it
+ * does not cover and CW_ERR_HIP if a grid barrier timed out. */
 int cw_generate(cw_model *m, const uint32_t *prompt, int n_prompt, int max_new, int start_pos,
-                int use_graph, uint32_t *out_tokens);
+                int mode, uint32_t *out_tokens);
 /* Launch n_steps more decode steps of the current generate state without
  * synchronising (for timing); cw_flush waits. */
-int cw_model_decode_async(cw_model *m, int n_steps, int use_graph);
+int cw_model_decode_async(cw_model *m, int n_steps, int mode);
+/* Per-phase timeline of one fused decode step (profile.rs:17-118 reports per
+ * kernel; the fused step is one kernel, so it reports per phase): runs one
+ * CW_STEP_FUSED step of the current generate state and writes the wall-clock
+ * stamps workgroup 0 took: [0] start, then per grid barrier e = 1..5L
+ * [2e] arrive and [2e+1] release, [10L+2] the end of the LM head, and from
+ * [10L+4] per phase (5 per layer, then the LM head) two stamps: after
+ * staging, after compute (20L+8 stamps in all); *tick_hz is the clock rate. */
+int cw_model_profile_step(cw_model *m, int64_t *ticks, int max_n, int *n_out, double *tick_hz);
 /* Reset the decode state to (token, pos) without touching the cache. */
 int cw_model_reset_state(cw_model *m, uint32_t token, int pos);
 /* Download the tokens produced so far by the device-resident loop. */

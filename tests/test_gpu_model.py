@@ -52,9 +52,9 @@ def test_tiny_reference_model(ctx):
     weights = mg.tiny_weights()
     m, o = build_pair(ctx, cfg, weights)
     prompt = np.array([1, 5, 9, 2], np.uint32)
-    for use_graph in (True, False, True):
-        toks = m.generate(prompt, 8, use_graph=use_graph)
-        assert np.array_equal(toks, z["tokens"]), (use_graph, toks, z["tokens"])
+    for mode in (cw.STEP_GRAPH, cw.STEP_EAGER, cw.STEP_GRAPH):
+        toks = m.generate(prompt, 8, mode=mode)
+        assert np.array_equal(toks, z["tokens"]), (mode, toks, z["tokens"])
     m2 = cw.Model(ctx, cfg)
     m2.set_weights(weights)
     m2.finalize()
@@ -63,6 +63,17 @@ def test_tiny_reference_model(ctx):
     teacher_forced(m, o, [1, 5, 9, 2] + list(z["tokens"][:7]))
     m.close()
     m2.close()
+
+
+def test_fused_step_refused_while_disabled(ctx):
+    """CW_STEP_FUSED is refused with an error, never launched."""
+    cfg = cw.make_config(2, 256, 4, 2, 128, 512, 1000, 8)
+    m = cw.Model(ctx, cfg)
+    m.load_synthetic(3)
+    m.finalize()
+    with pytest.raises(cw.CwError, match="fused decode step disabled"):
+        m.generate(np.array([1, 2], np.uint32), 2, mode=cw.STEP_FUSED)
+    m.close()
 
 
 def test_missing_tensor_is_an_error(ctx):
@@ -107,7 +118,7 @@ def test_qwen3_06b_token_loop(ctx):
     weights = cw.synthetic_weights(cfg, 2024)
     prompt = cw.synth_tokens(cw.synth_key(2024, "prompt"), P, cfg.vocab)
     m, o = build_pair(ctx, cfg, weights)
-    toks = m.generate(prompt, N, use_graph=True)
+    toks = m.generate(prompt, N, mode=cw.STEP_GRAPH)
     ref, margins = o.generate(prompt, N)
     first_diff = np.nonzero(toks != ref)[0]
     msg = "" if not first_diff.size else (
@@ -136,7 +147,7 @@ def test_qwen3_8b_decode_prefilled(ctx):
     m, o = build_pair(ctx, cfg, weights)
     m.prefill_kv(k, v, pre)
     o.prefill_kv(k, v, pre)
-    toks = m.generate(start, N, start_pos=pre, use_graph=True)
+    toks = m.generate(start, N, start_pos=pre, mode=cw.STEP_GRAPH)
     ref, margins = o.generate(start, N, start_pos=pre)
     first_diff = np.nonzero(toks != ref)[0]
     msg = "" if not first_diff.size else (
@@ -145,5 +156,115 @@ def test_qwen3_8b_decode_prefilled(ctx):
     # teacher-forced logits at the first 4 decode positions (same tokens as fed)
     worst = teacher_forced(m, o, [int(start[0])] + list(ref[:3]), start_pos=pre)
     print(f"\n[qwen3-8b] max |logit diff| = {worst:.3e}", flush=True)
+    m.close()
+    o.close()
+
+
+# ---------------------------------------------------------------- fused decode step
+
+# The persistent decode-step kernel raised an illegal memory access on its last
+# GPU run (test_fused_step_small_model[f32, 4 heads / 2 kv]); its cause is not
+# found yet, so the library refuses CW_STEP_FUSED and these tests stay skipped.
+FUSED_SKIP = pytest.mark.skip(reason="fused decode step disabled: unexplained illegal memory "
+                                     "access on its last GPU run")
+
+def small128(max_seq, kv_dtype=cw.CW_F32, n_heads=4, n_kv=2):
+    """A small model the fused step covers (head_dim 128)."""
+    return cw.make_config(2, 256, n_heads, n_kv, 128, 512, 1000, max_seq, kv_dtype, 1e-6, 1e6)
+
+
+@FUSED_SKIP
+@pytest.mark.parametrize("kv_dtype,n_heads,n_kv", [(cw.CW_F32, 4, 2), (cw.CW_F16, 8, 2),
+                                                   (cw.CW_F32, 2, 2), (cw.CW_F16, 8, 1)])
+def test_fused_step_small_model(ctx, kv_dtype, n_heads, n_kv):
+    """One persistent kernel per token: greedy ids equal the oracle's and the
+    graph path's; the last step's logits agree with the graph path's to
+    1e-4 of their range and with the oracle's to 1e-3 absolute."""
+    P, N = 5, 24
+    cfg = small128(P + N, kv_dtype, n_heads, n_kv)
+    weights = cw.synthetic_weights(cfg, 77)
+    prompt = cw.synth_tokens(cw.synth_key(77, "prompt"), P, cfg.vocab)
+    m, o = build_pair(ctx, cfg, weights)
+    ref, margins = o.generate(prompt, N)
+    g = m.generate(prompt, N, mode=cw.STEP_GRAPH)
+    lg = m.logits()
+    f = m.generate(prompt, N, mode=cw.STEP_FUSED)
+    lf = m.logits()
+    assert np.array_equal(f, ref), (f, ref, margins)
+    assert np.array_equal(g, ref)
+    assert np.max(np.abs(lf - lg)) <= 1e-4 * np.max(np.abs(lg))
+    # teacher-forced: the oracle's logits at the last fed position
+    fed = list(prompt) + list(ref[:N - 1])
+    o2 = orc.OracleModel(cfg, weights)
+    for i, t in enumerate(fed):
+        ol, _ = o2.step(int(t), i)
+    assert np.max(np.abs(lf - ol)) <= LOGIT_TOL
+    # a second fused run over the same positions gives the same bits
+    f2 = m.generate(prompt, N, mode=cw.STEP_FUSED)
+    assert np.array_equal(f2, f) and np.array_equal(m.logits(), lf)
+    m.close()
+    o.close()
+    o2.close()
+
+
+@FUSED_SKIP
+def test_fused_step_unsupported_shape_is_an_error(ctx):
+    cfg = cw.make_config(2, 64, 4, 2, 16, 128, 256, 12, cw.CW_F32, 1e-6, 1e6)
+    import make_golden as mg
+    m = cw.Model(ctx, cfg)
+    m.set_weights(mg.tiny_weights())
+    m.finalize()
+    with pytest.raises(cw.CwError, match="head_dim must be 128"):
+        m.generate(np.array([1, 5], np.uint32), 2, mode=cw.STEP_FUSED)
+    m.close()
+
+
+@FUSED_SKIP
+def test_fused_qwen3_06b_token_loop(ctx):
+    """Qwen3-0.6B shape through the fused step: identical greedy ids to the
+    oracle over 32 prompt + 128 generated tokens (f32 KV)."""
+    P, N = 32, 128
+    cfg = qwen3_06b(P + N)
+    weights = cw.synthetic_weights(cfg, 2024)
+    prompt = cw.synth_tokens(cw.synth_key(2024, "prompt"), P, cfg.vocab)
+    m, o = build_pair(ctx, cfg, weights)
+    toks = m.generate(prompt, N, mode=cw.STEP_FUSED)
+    ref, margins = o.generate(prompt, N)
+    first_diff = np.nonzero(toks != ref)[0]
+    msg = "" if not first_diff.size else (
+        f"first divergence at step {first_diff[0]}: margin {margins[first_diff[0]]:.3e}")
+    assert np.array_equal(toks, ref), msg
+    m.close()
+    o.close()
+
+
+@FUSED_SKIP
+def test_fused_qwen3_8b_decode_prefilled(ctx):
+    """Qwen3-8B shape through the fused step from a 4096-position f16 cache:
+    identical greedy ids to the oracle, and the last logits within 1e-3."""
+    pre, N = 4096, 16
+    cfg = qwen3_8b(pre + N)
+    weights = cw.synthetic_weights(cfg, 8008)
+    kv_n = cfg.n_layers * pre * cfg.n_kv_heads * cfg.head_dim
+    k = cw.synth_normal_f16(cw.synth_key(8008, "kv.k"), kv_n)
+    v = cw.synth_normal_f16(cw.synth_key(8008, "kv.v"), kv_n)
+    start = cw.synth_tokens(cw.synth_key(8008, "start"), 1, cfg.vocab)
+    m, o = build_pair(ctx, cfg, weights)
+    m.prefill_kv(k, v, pre)
+    o.prefill_kv(k, v, pre)
+    toks = m.generate(start, N, start_pos=pre, mode=cw.STEP_FUSED)
+    lf = m.logits()
+    ref, margins = o.generate(start, N, start_pos=pre)
+    first_diff = np.nonzero(toks != ref)[0]
+    msg = "" if not first_diff.size else (
+        f"first divergence at step {first_diff[0]}: margin {margins[first_diff[0]]:.3e}")
+    assert np.array_equal(toks, ref), msg
+    # the graph path over the same tokens ends with the same logits
+    g = m.generate(start, N, start_pos=pre, mode=cw.STEP_GRAPH)
+    assert np.array_equal(g, toks)
+    lg = m.logits()
+    print(f"\n[qwen3-8b fused] max |logit fused - graph| = {np.max(np.abs(lf - lg)):.3e}",
+          flush=True)
+    assert np.max(np.abs(lf - lg)) <= LOGIT_TOL
     m.close()
     o.close()
