@@ -125,6 +125,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--probe", action="store_true",
+                    help="for rocprofv3 --pmc runs: one 256 MiB device-to-device copy (the "
+                         "counter calibration), then 4 eager decode steps of the workload; "
+                         "prints no JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
@@ -149,6 +153,19 @@ def main():
     m.prefill_kv(k, v, PRE)
     start = int(cw.synth_tokens(cw.synth_key(8008, "start"), 1, cfg.vocab)[0])
     log(f"model ready in {time.perf_counter() - t:.1f}s")
+
+    if args.probe:
+        n = 256 << 20
+        src, dst = ctx.empty(n, np.uint8), ctx.empty(n, np.uint8)
+        cw.check(cw.lib().cw_copy(ctx.h, dst.ptr, src.ptr, n))
+        ctx.flush()
+        m.reset_state(start, PRE)
+        m.decode_async(4, mode=cw.STEP_EAGER)
+        ctx.flush()
+        log("probe done")
+        m.close()
+        ctx.close()
+        return
 
     m.reset_state(start, PRE)
     m.decode_async(W, mode=cw.STEP_GRAPH)
