@@ -7,9 +7,11 @@ with 4096 positions of N(0,1), batch 1.  Timed: K decode steps from position
 4096 (HIP-graph replay of the device-resident step), inputs resident in HBM.
 
 Prints one JSON line.  Extra fields: the roofline of the dominant kernel
-family, the Q4 GEMV (HIP events on the library stream around every launch of
-8 eager steps of the same workload), the whole-token byte roofline, the CPU
-oracle baseline on a bounded sample, and the Qwen3-0.6B-shape token loop.
+family, the Q4 GEMV (kernel start/end timestamps that the dispatch itself
+writes into HIP events, hipExtLaunchKernel, for every launch of 8 eager steps
+of the same workload on the library stream), its HBM traffic per launch from
+the committed rocprofv3 counter summary, the whole-token byte roofline, the
+CPU oracle baseline on a bounded sample, and the Qwen3-0.6B-shape token loop.
 
   python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -117,6 +119,24 @@ def bench_06b(ctx, warm=True):
     return (P + N - 1) / el, el
 
 
+TRAFFIC_MD = os.path.join(ROOT, "profiles", "q4_gemv_qwen3-8b-decode_hbm-traffic.md")
+
+
+def committed_gemv_traffic():
+    """HBM bytes per Q4 GEMV launch (FETCH_SIZE and WRITE_SIZE, calibrated,
+    averaged over one token's launches) from the committed rocprofv3 counter
+    summary, or (None, reason) when there is none."""
+    try:
+        with open(TRAFFIC_MD) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip().replace(",", "")), \
+                        "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, " + os.path.relpath(TRAFFIC_MD, ROOT)
+    except OSError:
+        pass
+    return None, "no committed counter summary"
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -183,8 +203,9 @@ def main():
     tok_s = K / el
     log(f"timed {K} steps in {el * 1e3:.2f} ms -> {tok_s:.1f} tok/s; first tokens {toks[:8]}")
 
-    # roofline of the dominant kernel family (the Q4 GEMVs): HIP events on the
-    # library stream around every launch of NP eager steps of the same workload
+    # roofline of the dominant kernel family (the Q4 GEMVs): every launch of NP
+    # eager steps of the same workload carries a start/stop event pair that
+    # its dispatch stamps with the kernel's own start and end times
     NP = 8
     m.reset_state(start, PRE)
     ctx.flush()
@@ -197,8 +218,9 @@ def main():
     gbytes = gemv_bytes_per_token(cfg)
     achieved = gbytes / (gemv_ms * 1e-3) / 1e9
     kernel_ms = sum(ms for _, ms in prof.values())
-    log("per-token kernel ms (eager, events): " +
+    log("per-token kernel ms (eager, kernel timestamps): " +
         ", ".join(f"{n}={ms:.3f}" for n, (_, ms) in prof.items()))
+    traffic, traffic_src = committed_gemv_traffic()
     bytes_avg = sum(step_bytes(cfg, PRE + i + 1, 2)[0] for i in range(K)) / K
 
     result = {
@@ -221,13 +243,14 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": traffic, "traffic_source": traffic_src,
                      "kernel": "q4_gemv_kernel (all 4 fused variants; 4 launches per layer "
                                "+ the LM head)",
                      "algorithmic_bytes_per_token": gbytes,
                      "avg_bytes_per_launch": round(gbytes / gemv_launches),
                      "avg_launch_us": round(gemv_ms * 1e3 / gemv_launches, 2),
                      "launches_per_token": gemv_launches},
+        "kernel_us_per_launch": {n: round(ms * 1e3 / c, 2) for n, (c, ms) in prof.items()},
         "token_roofline": {"algorithmic_bytes_per_token": round(bytes_avg),
                            "ideal_ms_at_peak": round(bytes_avg / (HBM_PEAK_GBS * 1e6), 4),
                            "kernel_ms_per_token_eager": round(kernel_ms, 4),

@@ -224,10 +224,13 @@ __global__ __launch_bounds__(64 * HPK) void attn_kernel(cwi::AttnArgs a, float s
         const int f = tid + i * C::THREADS;
         if (f < C::CP * C::U4_ROW) {
             const int row = f / C::U4_ROW, col = f % C::U4_ROW;
+            // select per component: a select of whole uint4 lvalues becomes a
+            // pointer select that forces kr/vr into scratch memory
             const bool live = c0 + row < seq;
-            const uint4 zero = make_uint4(0, 0, 0, 0);
-            *reinterpret_cast<uint4 *>(k_t + row * C::ROWP + col * 16) = live ? kr[i] : zero;
-            *reinterpret_cast<uint4 *>(v_t + row * C::ROWP + col * 16) = live ? vr[i] : zero;
+            uint4 kk = kr[i], vv = vr[i];
+            if (!live) kk = vv = make_uint4(0, 0, 0, 0);
+            *reinterpret_cast<uint4 *>(k_t + row * C::ROWP + col * 16) = kk;
+            *reinterpret_cast<uint4 *>(v_t + row * C::ROWP + col * 16) = vv;
         }
     }
     __syncthreads();

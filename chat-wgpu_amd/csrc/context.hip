@@ -171,6 +171,13 @@ void prof_end(cw_ctx *ctx) {
     if (r.stop) hipEventRecord(r.stop, ctx->stream);
 }
 
+void prof_events(cw_ctx *ctx, const char *label, hipEvent_t *start, hipEvent_t *stop) {
+    cw_prof_rec r{next_event(ctx), next_event(ctx), label};
+    ctx->prof.push_back(r);
+    *start = r.start;
+    *stop = r.stop;
+}
+
 }  // namespace cwi
 
 using namespace cwi;

@@ -1,6 +1,7 @@
 // Internal declarations shared by the HIP translation units of libchatwgpu.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -94,11 +95,36 @@ int ctx_rope_table(cw_ctx *ctx, float theta, int head_dim, int min_pos, const cw
 // Build the host table (f64 angles rounded to f32), layout [pos][hd/2].
 void rope_table_host(int max_pos, int head_dim, float theta, float *cos_t, float *sin_t);
 
-// Profiling hooks around a launch (no-ops unless profiling).
+// Profiling hooks around a launch (no-ops unless profiling): marker events
+// before and after it, so the interval also holds the dispatch overhead.
 void prof_begin(cw_ctx *ctx, const char *label);
 void prof_end(cw_ctx *ctx);
+// A profile record for the next launch and its two events (profiling only).
+void prof_events(cw_ctx *ctx, const char *label, hipEvent_t *start, hipEvent_t *stop);
 // Check the launch that was just enqueued.
 int launch_check(const char *what);
+
+template <typename T>
+struct same_type {
+    using type = T;
+};
+
+// Enqueue fn on ctx->stream.  While profiling, the dispatch itself stamps a
+// pair of events at the kernel's start and end (hipExtLaunchKernel), so the
+// profile holds kernel execution time, as a kernel trace does, with no
+// marker packets between launches.
+template <typename... KA>
+int launch(cw_ctx *ctx, const char *label, void (*fn)(KA...), dim3 grid, dim3 block,
+           unsigned lds, typename same_type<KA>::type... args) {
+    if (ctx->profiling) {
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        prof_events(ctx, label, &e0, &e1);
+        hipExtLaunchKernelGGL(fn, grid, block, lds, ctx->stream, e0, e1, 0, args...);
+    } else {
+        hipLaunchKernelGGL(fn, grid, block, lds, ctx->stream, args...);
+    }
+    return launch_check(label);
+}
 
 // f16 helpers on the host (IEEE binary16, round to nearest even).
 uint16_t f32_to_f16_bits(float f);

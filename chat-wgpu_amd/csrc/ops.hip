@@ -229,61 +229,42 @@ namespace cwi {
 
 int launch_rmsnorm(cw_ctx *ctx, const float *x, const float *w, int rows, int dim, float eps,
                    float *y) {
-    prof_begin(ctx, "rmsnorm");
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, ctx->stream, x, w, dim, eps,
-                       y);
-    prof_end(ctx);
-    return launch_check("rmsnorm");
+    return launch(ctx, "rmsnorm", rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, x, w, dim, eps,
+                  y);
 }
 
 int launch_rope(cw_ctx *ctx, const float *x, int rows, int hd, int pos, const float *cos_t,
                 const float *sin_t, float *y) {
     const int n = rows * (hd / 2);
-    prof_begin(ctx, "rope");
-    hipLaunchKernelGGL(rope_kernel, dim3((n + kThreads - 1) / kThreads), dim3(kThreads), 0,
-                       ctx->stream, x, rows, hd, pos, cos_t, sin_t, y);
-    prof_end(ctx);
-    return launch_check("rope");
+    return launch(ctx, "rope", rope_kernel, dim3((n + kThreads - 1) / kThreads), dim3(kThreads), 0,
+                  x, rows, hd, pos, cos_t, sin_t, y);
 }
 
 int launch_add(cw_ctx *ctx, const float *a, const float *b, int n, float *c) {
-    prof_begin(ctx, "ewise_add");
-    hipLaunchKernelGGL(add_kernel, dim3((n + kThreads - 1) / kThreads), dim3(kThreads), 0,
-                       ctx->stream, a, b, n, c);
-    prof_end(ctx);
-    return launch_check("ewise_add");
+    return launch(ctx, "ewise_add", add_kernel, dim3((n + kThreads - 1) / kThreads),
+                  dim3(kThreads), 0, a, b, n, c);
 }
 
 int launch_swiglu(cw_ctx *ctx, const float *g, const float *u, int n, float *out) {
-    prof_begin(ctx, "swiglu");
-    hipLaunchKernelGGL(swiglu_kernel, dim3((n + kThreads - 1) / kThreads), dim3(kThreads), 0,
-                       ctx->stream, g, u, n, out);
-    prof_end(ctx);
-    return launch_check("swiglu");
+    return launch(ctx, "swiglu", swiglu_kernel, dim3((n + kThreads - 1) / kThreads),
+                  dim3(kThreads), 0, g, u, n, out);
 }
 
 int launch_kv_write(cw_ctx *ctx, void *kc, void *vc, int kv_dtype, int pos, const int *pos_dev,
                     int kv_dim, const float *k, const float *v) {
     dim3 grid((kv_dim + kThreads - 1) / kThreads);
-    prof_begin(ctx, "kv_write");
     if (kv_dtype == CW_F16)
-        hipLaunchKernelGGL(kv_write_kernel<_Float16>, grid, dim3(kThreads), 0, ctx->stream,
-                           (_Float16 *)kc, (_Float16 *)vc, pos, pos_dev, kv_dim, k, v);
-    else
-        hipLaunchKernelGGL(kv_write_kernel<float>, grid, dim3(kThreads), 0, ctx->stream,
-                           (float *)kc, (float *)vc, pos, pos_dev, kv_dim, k, v);
-    prof_end(ctx);
-    return launch_check("kv_write");
+        return launch(ctx, "kv_write", kv_write_kernel<_Float16>, grid, dim3(kThreads), 0,
+                      (_Float16 *)kc, (_Float16 *)vc, pos, pos_dev, kv_dim, k, v);
+    return launch(ctx, "kv_write", kv_write_kernel<float>, grid, dim3(kThreads), 0, (float *)kc,
+                  (float *)vc, pos, pos_dev, kv_dim, k, v);
 }
 
 int launch_embed(cw_ctx *ctx, const float *table, int vocab, int dim, const uint32_t *tok_dev,
                  float *out) {
     int blocks = (dim + kThreads - 1) / kThreads;
-    prof_begin(ctx, "embed");
-    hipLaunchKernelGGL(embed_kernel, dim3(blocks), dim3(kThreads), 0, ctx->stream, table, vocab,
-                       dim, tok_dev, out);
-    prof_end(ctx);
-    return launch_check("embed");
+    return launch(ctx, "embed", embed_kernel, dim3(blocks), dim3(kThreads), 0, table, vocab, dim,
+                  tok_dev, out);
 }
 
 size_t argmax_scratch_bytes(int n) {
@@ -299,14 +280,10 @@ int launch_argmax(cw_ctx *ctx, const float *logits, int n, uint32_t *out_dev, vo
     const int per_block = (n + blocks - 1) / blocks;
     float *pv = (float *)scratch;
     uint32_t *pi = (uint32_t *)(pv + kArgmaxBlocks);
-    prof_begin(ctx, "argmax");
-    hipLaunchKernelGGL(argmax_partial_kernel, dim3(blocks), dim3(kThreads), 0, ctx->stream, logits,
-                       n, per_block, pv, pi);
-    CW_TRY(launch_check("argmax_partial"));
-    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kThreads), 0, ctx->stream, pv, pi, blocks,
-                       out_dev, state, prompt_dev, tokens_out_dev);
-    prof_end(ctx);
-    return launch_check("argmax_final");
+    CW_TRY(launch(ctx, "argmax", argmax_partial_kernel, dim3(blocks), dim3(kThreads), 0, logits,
+                  n, per_block, pv, pi));
+    return launch(ctx, "argmax", argmax_final_kernel, dim3(1), dim3(kThreads), 0, pv, pi, blocks,
+                  out_dev, state, prompt_dev, tokens_out_dev);
 }
 
 }  // namespace cwi
@@ -372,11 +349,8 @@ int cw_hbm_read_probe(cw_ctx *ctx, const void *buf, size_t bytes, int blocks, ui
     CW_CHECK_ARG(((uintptr_t)buf & 15) == 0 && bytes >= 16,
                  "cw_hbm_read_probe: buf must be 16-byte aligned and bytes >= 16");
     CW_CHECK_ARG(blocks > 0 && blocks <= 65536, "cw_hbm_read_probe: blocks=%d", blocks);
-    prof_begin(ctx, "hbm_read_probe");
-    hipLaunchKernelGGL(read_probe_kernel, dim3(blocks), dim3(kThreads), 0, ctx->stream,
-                       (const uint4 *)buf, bytes / 16, out_dev);
-    prof_end(ctx);
-    return launch_check("hbm_read_probe");
+    return launch(ctx, "hbm_read_probe", read_probe_kernel, dim3(blocks), dim3(kThreads), 0,
+                  (const uint4 *)buf, bytes / 16, out_dev);
 }
 
 }  // extern "C"

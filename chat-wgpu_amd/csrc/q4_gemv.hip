@@ -384,10 +384,7 @@ int launch_q4_gemv(cw_ctx *ctx, XSrc xs, Epi epi, const GemvArgs &a) {
     int grid = (n_tiles + kWaves - 1) / kWaves;
     const int resident = ctx->n_cu * occ;
     if (grid > resident) grid = resident;
-    prof_begin(ctx, label_of(xs, epi));
-    hipLaunchKernelGGL(fn, dim3(grid), dim3(kThreads), lds, ctx->stream, a, n_tiles);
-    prof_end(ctx);
-    return launch_check(label_of(xs, epi));
+    return launch(ctx, label_of(xs, epi), fn, dim3(grid), dim3(kThreads), lds, a, n_tiles);
 }
 
 }  // namespace cwi
