@@ -103,7 +103,16 @@ def cpu_baseline_8b(cfg, weights, k, v, start_tok, budget_s):
     return n / el, n, el
 
 
+def gemv_profile(prof, n_steps):
+    """(ms per token, launches per token) of the q4_gemv labels of a profile."""
+    g = [(c, ms) for name, c, ms in prof if name.startswith("q4_gemv")]
+    return sum(ms for _, ms in g) / n_steps, sum(c for c, _ in g) / n_steps
+
+
 def bench_06b(ctx, warm=True):
+    """Qwen3-0.6B-shape token loop (32 prompt + 128 greedy, f32 KV, graph
+    replay), and the same model's Q4 GEMV launches of one decode token timed
+    by kernel timestamps over 8 eager steps (the GEMVs of one 0.6B step)."""
     P, N = 32, 128
     cfg = cw.make_config(28, 1024, 16, 8, 128, 3072, 151936, P + N, cw.CW_F32, 1e-6, 1e6)
     m = cw.Model(ctx, cfg)
@@ -115,8 +124,73 @@ def bench_06b(ctx, warm=True):
     t0 = time.perf_counter()
     m.generate(prompt, N, mode=cw.STEP_GRAPH)
     el = time.perf_counter() - t0
+    NP = 8
+    m.reset_state(int(prompt[-1]), P)
+    ctx.flush()
+    ctx.profile_begin()
+    m.decode_async(NP, mode=cw.STEP_EAGER)
+    gms, gl = gemv_profile(ctx.profile_report(), NP)
     m.close()
-    return (P + N - 1) / el, el
+    return (P + N - 1) / el, el, gemv_bytes_per_token(cfg), gms, gl
+
+
+def bench_single_gemv(ctx, out_f=3072, in_f=1024, pool_bytes=600 << 20, passes=3):
+    """One Q4_0 GEMV y[out_f] = W x[in_f] (x ~ N(0,1), d = f16(|N(0,0.02)|),
+    uniform nibbles) over a rotating pool of weight copies larger than the
+    256 MB last-level cache, so every launch streams its weights from HBM.
+    Kernel time from the dispatch's own start/end timestamps; returns
+    (us per launch, algorithmic bytes per launch, copies in the pool)."""
+    s, q = cw.synth_q4(cw.synth_key(7, "c0.w"), out_f, in_f)
+    x = cw.synth_normal_f32(cw.synth_key(7, "c0.x"), in_f)
+    wb = s.nbytes + q.nbytes
+    n = max(2, pool_bytes // wb)
+    sd0, qd0 = ctx.storage(s), ctx.storage(q)
+    pool = []
+    for _ in range(n):
+        sd, qd = ctx.empty(s.shape, np.uint16), ctx.empty(q.shape, np.uint8)
+        cw.check(cw.lib().cw_copy(ctx.h, sd.ptr, sd0.ptr, s.nbytes))
+        cw.check(cw.lib().cw_copy(ctx.h, qd.ptr, qd0.ptr, q.nbytes))
+        pool.append((sd, qd))
+    xd, yd = ctx.storage(x), ctx.empty(out_f, np.float32)
+    for sd, qd in pool:  # warm
+        ctx.q4_gemv(xd, sd, qd, in_f, out_f, y=yd)
+    ctx.flush()
+    ctx.profile_begin()
+    for _ in range(passes):
+        for sd, qd in pool:
+            ctx.q4_gemv(xd, sd, qd, in_f, out_f, y=yd)
+    _, cnt, ms = ctx.profile_report()[0]
+    for sd, qd in pool:
+        ctx.free(sd)
+        ctx.free(qd)
+    for d in (sd0, qd0, xd, yd):
+        ctx.free(d)
+    return ms * 1e3 / cnt, q4_bytes(out_f, in_f) + 4 * in_f + 4 * out_f, n
+
+
+def cpu_single_gemv(out_f=3072, in_f=1024, budget_s=1.0):
+    """The reference's CPU GEMV paths restated in the oracle, one thread: the
+    sequential Q4 dequant-dot (src/main.rs:133-150) and naive_matmul at m=1
+    on the dequantized f32 weights (examples/bench/src/lib.rs:221-233).
+    Returns (us per q4 dot GEMV, us per naive_matmul GEMV)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    orc.set_threads(1)
+    s, q = cw.synth_q4(cw.synth_key(7, "c0.w"), out_f, in_f)
+    x = cw.synth_normal_f32(cw.synth_key(7, "c0.x"), in_f)
+    wt = np.ascontiguousarray(orc.dequant_q4_0_soa(s, q).reshape(out_f, in_f).T)  # B [k, n]
+
+    def timed(fn):
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                return el / n * 1e6
+    t_q4 = timed(lambda: orc.q4_gemv(x, s, q, in_f, out_f))
+    t_nm = timed(lambda: orc.naive_matmul(x, wt, 1, in_f, out_f))
+    return t_q4, t_nm
 
 
 TRAFFIC_MD = os.path.join(ROOT, "profiles", "q4_gemv_qwen3-8b-decode_hbm-traffic.md")
@@ -271,10 +345,34 @@ def main():
     m.close()
 
     if not args.no_extras:
-        tps06, el06 = bench_06b(ctx)
-        result["extras"]["qwen3_0.6b_token_loop_tok_s"] = round(tps06, 1)
-        result["extras"]["qwen3_0.6b_token_loop"] = ("32 prompt + 128 greedy, f32 KV, 159 "
-                                                     "forwards incl. prompt, HIP graph")
+        tps06, el06, gb06, gms06, gl06 = bench_06b(ctx)
+        ex = result["extras"]
+        ex["qwen3_0.6b_token_loop_tok_s"] = round(tps06, 1)
+        ex["qwen3_0.6b_token_loop"] = ("32 prompt + 128 greedy, f32 KV, 159 forwards incl. "
+                                       "prompt, HIP graph")
+        ex["qwen3_0.6b_step_gemvs"] = {
+            "workload": "one Qwen3-0.6B-shape decode step's Q4_0 GEMVs (28 layers x "
+                        "QKV, O, gate/up, down + LM head 1024->151936), kernel timestamps "
+                        "over 8 eager steps",
+            "algorithmic_bytes": gb06, "launches": gl06, "us": round(gms06 * 1e3, 2),
+            "GB_s": round(gb06 / (gms06 * 1e-3) / 1e9, 1),
+            "frac_of_peak": round(gb06 / (gms06 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        us1, b1, n1 = bench_single_gemv(ctx)
+        ex["single_q4_gemv_3072x1024"] = {
+            "workload": f"y[3072] = W x[1024], Q4_0, rotating pool of {n1} weight copies "
+                        "(> the 256 MB last-level cache), kernel timestamps",
+            "algorithmic_bytes": b1, "us_per_launch": round(us1, 3),
+            "GB_s": round(b1 / (us1 * 1e-6) / 1e9, 1),
+            "frac_of_peak": round(b1 / (us1 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        if not args.no_cpu_baseline:
+            t_q4, t_nm = cpu_single_gemv()
+            ex["single_q4_gemv_3072x1024"]["cpu_baseline"] = {
+                "q4_dot_us": round(t_q4, 1), "naive_matmul_us": round(t_nm, 1), "cores": 1,
+                "kind": "port",
+                "sample": "the reference's sequential Q4 dequant-dot (main.rs:133-150) and "
+                          "naive_matmul at m=1 on the dequantized weights "
+                          "(examples/bench/src/lib.rs:221-233), C restatement, 1 thread, "
+                          "repeated for 1 s each"}
     ctx.close()
     print(json.dumps(result), flush=True)
 

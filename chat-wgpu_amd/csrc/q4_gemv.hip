@@ -11,13 +11,16 @@
 // Work split: a wave64 covers 64 blocks per step.  G = lanes per row (the
 // largest power of two <= 64 dividing K/32); 64/G rows share a wave step.
 // A wave tile is R row slots x all K; waves walk wave tiles over a
-// persistent grid of 1024-thread workgroups (one per CU), so the activation
-// is staged into LDS once per CU: [8][K/32] float4 (conflict-free: lane b
-// reads float4 i of block b) plus the per-block sums sum_j x_j.
+// persistent grid of 1024-thread workgroups (two per CU, all resident ones
+// for the LM head), so the activation is staged into LDS once per
+// workgroup: [8][K/32] float4 (conflict-free: lane b reads float4 i of block
+// b) plus the per-block sums sum_j x_j.
 //
 // Latency: every wave issues the loads of its first (tile, step) group before
 // the activation is staged, and each iteration issues the next group's loads
-// (crossing tile boundaries) before computing the current one.
+// (crossing tile boundaries) before computing the current one.  Latency is
+// hidden by occupancy (32 waves per CU within 64 VGPRs) rather than by a deep
+// per-wave register ring, which measured slower.
 //
 // Nibble decode costs 5 VALU ops per 8 weights: AND-ing a quant dword with
 // 0x000F000F / 0x00F000F0 (and the same after one >>8) leaves two f16
@@ -32,6 +35,7 @@
 // staging.  Optional epilogues: residual add (ewise.wgsl:9-13) and SwiGLU of
 // a gate/up row pair (glu.wgsl:22-26).
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 
@@ -115,8 +119,12 @@ __device__ __forceinline__ void load_group(const GemvArgs &a, int nb, int wt, in
     }
 }
 
-template <int G, int R, int XS, int EPI>
-__global__ __launch_bounds__(kThreads) void q4_gemv_kernel(GemvArgs a, int n_wave_tiles) {
+// Occupancy over prefetch depth: at most 64 VGPRs (8 waves per SIMD, two or
+// more workgroups per CU) with PD = 1 or 2 groups in flight per wave streams
+// faster than one workgroup per CU with a deep register ring (measured on
+// MI355X: 13-26 % less time on the 4096- and 12288-wide layers).
+template <int G, int R, int XS, int EPI, int PD>
+__global__ __launch_bounds__(kThreads, 8) void q4_gemv_kernel(GemvArgs a, int n_wave_tiles) {
     using T = Tile<G, R, EPI>;
     extern __shared__ float4 lds4[];
     __shared__ float red[kWaves];
@@ -140,7 +148,6 @@ __global__ __launch_bounds__(kThreads) void q4_gemv_kernel(GemvArgs a, int n_wav
 
     // a ring of PD (tile, block) groups in flight per wave, issued before the
     // activation is staged; slot u always holds group it with it % PD == u
-    constexpr int PD = R == 4 ? 2 : R == 2 ? 5 : 10;  // fits 128 VGPRs (1024-thread groups)
     uint4 qv[PD][R];
     uint32_t dv[PD][R];
     int lk = 0, lstep = 0;  // next group to load
@@ -200,20 +207,19 @@ __global__ __launch_bounds__(kThreads) void q4_gemv_kernel(GemvArgs a, int n_wav
         for (int u = 0; u < PD; ++u) {
             if (base + u < total) {
                 const int b = s + step * G;
-                float4 xv[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) xv[i] = lds4[i * nb + b];
                 const float sxb = sx[b];
                 // one accumulator per (row, quant dword): independent fma_mix
-                // chains interleave without dependency stalls
+                // chains interleave without dependency stalls; x is read per
+                // dword (2 float4) to keep the register budget
                 float sum[R][4];
 #pragma unroll
                 for (int w = 0; w < 4; ++w) {
+                    const float4 xl = lds4[w * nb + b], xh = lds4[(4 + w) * nb + b];
 #pragma unroll
                     for (int r = 0; r < R; ++r) {
                         const uint4 q = qv[u][r];
                         const uint32_t dw = w == 0 ? q.x : w == 1 ? q.y : w == 2 ? q.z : q.w;
-                        sum[r][w] = dot_word(dw, xv[w], xv[4 + w], 0.0f);
+                        sum[r][w] = dot_word(dw, xl, xh, 0.0f);
                     }
                 }
 #pragma unroll
@@ -270,37 +276,40 @@ __global__ __launch_bounds__(kThreads) void q4_gemv_kernel(GemvArgs a, int n_wav
 
 typedef void (*gemv_fn)(GemvArgs, int);
 
-template <int G, int R, int XS>
+template <int G, int R, int XS, int PD>
 gemv_fn pick_epi(int epi) {
     switch (epi) {
-        case cwi::EPI_STORE: return q4_gemv_kernel<G, R, XS, cwi::EPI_STORE>;
-        case cwi::EPI_ADD: return q4_gemv_kernel<G, R, XS, cwi::EPI_ADD>;
+        case cwi::EPI_STORE: return q4_gemv_kernel<G, R, XS, cwi::EPI_STORE, PD>;
+        case cwi::EPI_ADD: return q4_gemv_kernel<G, R, XS, cwi::EPI_ADD, PD>;
         default:
-            if constexpr (R % 2 == 0) return q4_gemv_kernel<G, R, XS, cwi::EPI_SWIGLU>;
+            if constexpr (R % 2 == 0) return q4_gemv_kernel<G, R, XS, cwi::EPI_SWIGLU, PD>;
             return nullptr;
     }
 }
 
-template <int G, int R>
+template <int G, int R, int PD>
 gemv_fn pick_xs(int xs, int epi) {
-    return xs == cwi::XS_RMSNORM ? pick_epi<G, R, cwi::XS_RMSNORM>(epi)
-                                 : pick_epi<G, R, cwi::XS_PLAIN>(epi);
+    return xs == cwi::XS_RMSNORM ? pick_epi<G, R, cwi::XS_RMSNORM, PD>(epi)
+                                 : pick_epi<G, R, cwi::XS_PLAIN, PD>(epi);
 }
 
+// PD: one group in flight per wave, two for single-row tiles of long rows
+// (steps per tile S >= 4), where it measured faster.
 template <int G>
-gemv_fn pick_r(int r, int xs, int epi) {
-    return r == 4 ? pick_xs<G, 4>(xs, epi) : r == 2 ? pick_xs<G, 2>(xs, epi) : pick_xs<G, 1>(xs, epi);
+gemv_fn pick_r(int r, int xs, int epi, bool deep) {
+    if (r == 2) return pick_xs<G, 2, 1>(xs, epi);
+    return deep ? pick_xs<G, 1, 2>(xs, epi) : pick_xs<G, 1, 1>(xs, epi);
 }
 
-gemv_fn pick(int g, int r, int xs, int epi) {
+gemv_fn pick(int g, int r, int xs, int epi, bool deep) {
     switch (g) {
-        case 64: return pick_r<64>(r, xs, epi);
-        case 32: return pick_r<32>(r, xs, epi);
-        case 16: return pick_r<16>(r, xs, epi);
-        case 8: return pick_r<8>(r, xs, epi);
-        case 4: return pick_r<4>(r, xs, epi);
-        case 2: return pick_r<2>(r, xs, epi);
-        default: return pick_r<1>(r, xs, epi);
+        case 64: return pick_r<64>(r, xs, epi, deep);
+        case 32: return pick_r<32>(r, xs, epi, deep);
+        case 16: return pick_r<16>(r, xs, epi, deep);
+        case 8: return pick_r<8>(r, xs, epi, deep);
+        case 4: return pick_r<4>(r, xs, epi, deep);
+        case 2: return pick_r<2>(r, xs, epi, deep);
+        default: return pick_r<1>(r, xs, epi, deep);
     }
 }
 
@@ -360,30 +369,26 @@ int launch_q4_gemv(cw_ctx *ctx, XSrc xs, Epi epi, const GemvArgs &a) {
         const int rows = nr * rps;
         return (a.N + rows - 1) / rows;
     };
-    // R (row slots per wave tile): balance tiles over the chip's waves first
-    // (a wave with one tile more than the rest sets the kernel time), then
-    // prefer the larger R (fewer LDS reads of x per weight byte)
-    const int waves = ctx->n_cu * kWaves;
-    int r = 0;
-    double best = -1.0;
-    for (int cand : {4, 2, 1}) {
-        if (epi == EPI_SWIGLU && cand == 1) continue;
-        const int t = tiles_for(cand);
-        const int rounds = (t + waves - 1) / waves;
-        const double eff = (double)t / ((double)rounds * waves);  // mean / max tiles per wave
-        if (eff > best + 0.05) {
-            best = eff;
-            r = cand;
-        }
-    }
+    // R (row slots per wave tile) and the grid, as measured fastest on MI355X
+    // over the Qwen3 shapes: two-row tiles (gate/up pairs for SwiGLU) unless
+    // that leaves more than a quarter of the CUs without a workgroup, in which
+    // case single rows (e.g. 4096 x 4096: 4.8 us against 5.8); grids of two
+    // workgroups per CU, four for long streams (>= 8 tiles per wave of two
+    // workgroups per CU, e.g. the LM head: 62 us against 66).
+    const int r = (epi == EPI_SWIGLU ||
+                   4 * ((tiles_for(2) + kWaves - 1) / kWaves) >= 3 * ctx->n_cu)
+                      ? 2
+                      : 1;
     const int n_tiles = tiles_for(r);
-    gemv_fn fn = pick(g, r, xs, epi);
+    gemv_fn fn = pick(g, r, xs, epi, nb / g >= 4);
     const int lds = nb * 132;
     int occ = 1;
-    CW_TRY(occupancy(fn, lds, &occ));
+    CW_TRY(occupancy(fn, lds, &occ));  // raises the kernel's LDS limit
+    (void)occ;
+    const bool long_stream = n_tiles >= 16 * ctx->n_cu * kWaves;
     int grid = (n_tiles + kWaves - 1) / kWaves;
-    const int resident = ctx->n_cu * occ;
-    if (grid > resident) grid = resident;
+    const int cap = (long_stream ? 4 : 2) * ctx->n_cu;
+    if (grid > cap) grid = cap;
     return launch(ctx, label_of(xs, epi), fn, dim3(grid), dim3(kThreads), lds, a, n_tiles);
 }
 

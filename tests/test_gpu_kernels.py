@@ -253,6 +253,8 @@ ATTN_CASES = [  # (n_heads, n_kv, hd, seq, f16)
     (16, 8, 128, 1, False), (16, 8, 128, 33, False), (16, 8, 128, 128, False),
     (16, 8, 128, 129, True), (4, 2, 16, 9, False), (8, 8, 64, 300, True),
     (8, 1, 32, 257, False), (16, 2, 256, 200, True), (64, 8, 128, 1000, True),
+    # more than 256 chunks per head: the merge's multi-pass (max, sum) loops
+    (32, 8, 128, 9000, False),
 ]
 
 
@@ -266,6 +268,27 @@ def test_attention_vs_oracle(ctx, rng, nh, nkv, hd, seq, f16):
     ref = orc.attention(q, k, v, f16, nh, nkv, seq, hd)
     vmax = np.max(np.abs(v.view(np.float16) if f16 else v))
     assert np.max(np.abs(o - ref)) <= 1e-5 * vmax
+
+
+def test_attention_repeated_calls(ctx, rng):
+    """Calls of other shapes, single-chunk calls and other kernels that reuse
+    the context scratch (argmax) in between leave later calls exact."""
+    cases = [(32, 8, 128, 700, True), (16, 8, 128, 5, False), (8, 2, 64, 900, False),
+             (32, 8, 128, 4100, True), (16, 4, 128, 300, True)]
+    logits = rng.standard_normal(151936).astype(np.float32)
+    ld = ctx.storage(logits)
+    for rep in range(2):
+        for nh, nkv, hd, seq, f16 in cases:
+            q = rng.standard_normal(nh * hd).astype(np.float32) * 0.3
+            k, v = _kv(rng, seq, nkv, hd, f16)
+            dt = cw.CW_F16 if f16 else cw.CW_F32
+            o = ctx.attention(ctx.storage(q), ctx.storage(k), ctx.storage(v), dt, nh, nkv, seq,
+                              hd).download()
+            ref = orc.attention(q, k, v, f16, nh, nkv, seq, hd)
+            vmax = np.max(np.abs(v.view(np.float16) if f16 else v))
+            assert np.max(np.abs(o - ref)) <= 1e-5 * vmax, (rep, nh, nkv, hd, seq, f16)
+            # argmax reuses the context scratch that holds attention partials
+            assert int(ctx.argmax(ld, logits.size).download()[0]) == int(np.argmax(logits))
 
 
 def test_attention_constant_keys_mean(ctx, rng):
