@@ -34,7 +34,9 @@
 namespace {
 
 constexpr int kMaxChunkSpan = 32768;  // max_seq limit
-constexpr int kMergeThreads = 256;
+// 512 threads: 4 chunk slices x 32 loads per thread cover the 68 chunks of a
+// 4352-position cache in one pass (256 threads took two: 5.6 us against 4.3)
+constexpr int kMergeThreads = 512;
 
 template <typename KVT, int HD, int HPK>
 struct Cfg {
