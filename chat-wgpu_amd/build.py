@@ -16,8 +16,8 @@ BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libchatwgpu.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["context.hip", "q4_gemv.hip", "ops.hip", "attention.hip", "decode_step.hip", "host_utils.cpp",
-           "model.cpp"]
+SOURCES = ["context.hip", "q4_gemv.hip", "ops.hip", "attention.hip", "decode_step.hip", "prefill.hip",
+           "host_utils.cpp", "model.cpp"]
 
 # No packed FP32 (v_pk_*_f32): some forms have produced wrong results on these boxes.
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",

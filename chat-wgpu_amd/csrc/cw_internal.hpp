@@ -197,6 +197,33 @@ size_t argmax_scratch_bytes(int n);
 int launch_argmax(cw_ctx *ctx, const float *logits, int n, uint32_t *out_dev, void *scratch,
                   GenState *state, const uint32_t *prompt_dev, uint32_t *tokens_out_dev);
 
+// ---- batched prefill (M positions per launch)
+
+// y[M][N] = x[M][K] . W[N][K]^T with x given as bf16 hi/lo rows and W split
+// GGUF Q4_0; EPI_SWIGLU reads a second matrix (B) and stores silu(A x) * (B x).
+struct GemmArgs {
+    const uint16_t *xhi, *xlo;  // [M][K] bf16 bits
+    const uint16_t *sA;
+    const uint8_t *qA;
+    const uint16_t *sB;
+    const uint8_t *qB;
+    const float *resid;  // EPI_ADD: [M][N]
+    float *y;            // [M][N]
+    int M, N, K;
+};
+// token ids on the device (validated < vocab by the caller)
+int launch_embed_rows(cw_ctx *ctx, const float *table, int dim, const uint32_t *tok_dev, int n,
+                      float *out);
+int launch_split_rows(cw_ctx *ctx, const float *x, const float *norm_w, float eps, int rows, int K,
+                      uint16_t *hi, uint16_t *lo);
+int launch_q4_gemm(cw_ctx *ctx, Epi epi, const GemmArgs &a);
+int launch_qk_rope_kv(cw_ctx *ctx, const float *qkv, const float *qn, const float *kn, float eps,
+                      const float *cos_t, const float *sin_t, int M, int n_heads, int n_kv,
+                      int start, int kv_dtype, float *q_out, void *kc, void *vc);
+// causal attention of positions start..start+M-1 over an f16 cache, head_dim 128
+int launch_attn_prefill(cw_ctx *ctx, const float *q, const void *kc, const void *vc, int M,
+                        int n_heads, int n_kv, int start, float *out);
+
 // ---- the fused decode step (one persistent cooperative kernel per token)
 
 constexpr int kStepMaxKv = 32;

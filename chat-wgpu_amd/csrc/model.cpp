@@ -14,6 +14,7 @@
 // valid for every token and is captured once as a HIP graph and replayed
 // (the reference keeps "the same op sequence every token", mod.rs:78-81).
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -68,6 +69,13 @@ struct cw_model {
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
     std::vector<void *> allocs;
+
+    // batched prefill buffers, sized for pf_cap positions (grown on demand)
+    int pf_cap = 0;
+    float *pf_hidden = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_attn = nullptr,
+          *pf_act = nullptr;
+    uint16_t *pf_hi = nullptr, *pf_lo = nullptr;
+    std::vector<void *> pf_allocs;
 
     // fused decode step (one persistent kernel per token)
     const char *fused_unsupported = nullptr;
@@ -370,6 +378,79 @@ int setup_fused(cw_model *m) {
     return CW_OK;
 }
 
+// Batched prefill buffers for n positions.
+int ensure_prefill(cw_model *m, int n) {
+    if (n <= m->pf_cap) return CW_OK;
+    CW_HIP(hipStreamSynchronize(m->ctx->stream));
+    for (void *p : m->pf_allocs) CW_HIP(hipFree(p));
+    m->pf_allocs.clear();
+    m->pf_cap = 0;
+    const auto &c = m->cfg;
+    const size_t wide = std::max({(size_t)c.dim, (size_t)m->q_dim, (size_t)c.hidden});
+    auto al = [&](size_t bytes, void **out) -> int {
+        CW_HIP(hipMalloc(out, bytes));
+        m->pf_allocs.push_back(*out);
+        return CW_OK;
+    };
+    CW_TRY(al((size_t)n * c.dim * 4, (void **)&m->pf_hidden));
+    CW_TRY(al((size_t)n * (m->q_dim + 2 * m->kv_dim) * 4, (void **)&m->pf_qkv));
+    CW_TRY(al((size_t)n * m->q_dim * 4, (void **)&m->pf_q));
+    CW_TRY(al((size_t)n * m->q_dim * 4, (void **)&m->pf_attn));
+    CW_TRY(al((size_t)n * c.hidden * 4, (void **)&m->pf_act));
+    CW_TRY(al((size_t)n * wide * 2, (void **)&m->pf_hi));
+    CW_TRY(al((size_t)n * wide * 2, (void **)&m->pf_lo));
+    m->pf_cap = n;
+    return CW_OK;
+}
+
+// One linear layer of the batched forward: rows of x (optionally
+// RMS-normalised) through a Q4_0 matrix pair or single matrix.
+int pf_linear(cw_model *m, const float *x, const float *norm_w, int n, int K, Epi epi,
+              const Q4W &w, const Q4W *w2, const float *resid, float *y) {
+    CW_TRY(launch_split_rows(m->ctx, x, norm_w, m->cfg.eps, n, K, m->pf_hi, m->pf_lo));
+    GemmArgs a{};
+    a.xhi = m->pf_hi;
+    a.xlo = m->pf_lo;
+    a.sA = w.s;
+    a.qA = w.q;
+    if (w2) {
+        a.sB = w2->s;
+        a.qB = w2->q;
+    }
+    a.resid = resid;
+    a.y = y;
+    a.M = n;
+    a.N = w.out_f;
+    a.K = K;
+    return launch_q4_gemm(m->ctx, epi, a);
+}
+
+// Forward of n positions start..start+n-1 (tokens in m->prompt_dev) through
+// every layer with the batched kernels; leaves the hidden rows in pf_hidden.
+int enqueue_prefill(cw_model *m, int n, int start) {
+    cw_ctx *ctx = m->ctx;
+    const auto &c = m->cfg;
+    CW_TRY(launch_embed_rows(ctx, m->embed, c.dim, m->prompt_dev, n, m->pf_hidden));
+    for (int i = 0; i < c.n_layers; ++i) {
+        Layer &L = m->layers[i];
+        void *kc = (char *)m->kcache + (size_t)i * m->kv_layer_bytes;
+        void *vc = (char *)m->vcache + (size_t)i * m->kv_layer_bytes;
+        CW_TRY(pf_linear(m, m->pf_hidden, L.attn_norm, n, c.dim, EPI_STORE, L.qkv, nullptr,
+                         nullptr, m->pf_qkv));
+        CW_TRY(launch_qk_rope_kv(ctx, m->pf_qkv, L.q_norm, L.k_norm, c.eps, m->cos_t, m->sin_t, n,
+                                 c.n_heads, c.n_kv_heads, start, c.kv_dtype, m->pf_q, kc, vc));
+        CW_TRY(launch_attn_prefill(ctx, m->pf_q, kc, vc, n, c.n_heads, c.n_kv_heads, start,
+                                   m->pf_attn));
+        CW_TRY(pf_linear(m, m->pf_attn, nullptr, n, m->q_dim, EPI_ADD, L.wo, nullptr,
+                         m->pf_hidden, m->pf_hidden));
+        CW_TRY(pf_linear(m, m->pf_hidden, L.ffn_norm, n, c.dim, EPI_SWIGLU, L.gate, &L.up,
+                         nullptr, m->pf_act));
+        CW_TRY(pf_linear(m, m->pf_act, nullptr, n, c.hidden, EPI_ADD, L.down, nullptr,
+                         m->pf_hidden, m->pf_hidden));
+    }
+    return CW_OK;
+}
+
 int set_state(cw_model *m, const GenState &s) {
     CW_HIP(hipMemcpyAsync(m->state, &s, sizeof s, hipMemcpyHostToDevice, m->ctx->stream));
     CW_HIP(hipStreamSynchronize(m->ctx->stream));
@@ -478,6 +559,7 @@ int cw_model_destroy(cw_model *m) {
     if (m->graph_exec) hipGraphExecDestroy(m->graph_exec);
     if (m->graph) hipGraphDestroy(m->graph);
     for (void *p : m->allocs) hipFree(p);
+    for (void *p : m->pf_allocs) hipFree(p);
     delete m;
     return CW_OK;
 }
@@ -670,6 +752,54 @@ int cw_generate(cw_model *m, const uint32_t *prompt, int n_prompt, int max_new, 
                           m->ctx->stream));
     CW_HIP(hipStreamSynchronize(m->ctx->stream));
     return check_fused(m);
+}
+
+int cw_model_prefill(cw_model *m, const uint32_t *tokens, int n, int start_pos,
+                     uint32_t *next_token) {
+    CW_CHECK_ARG(m && tokens, "cw_model_prefill: null argument");
+    CW_TRY(require_final(m, "cw_model_prefill"));
+    const auto &c = m->cfg;
+    CW_CHECK_ARG(n >= 1 && start_pos >= 0 && (long)start_pos + n <= c.max_seq,
+                 "cw_model_prefill: positions [%d, %ld) outside max_seq %d", start_pos,
+                 (long)start_pos + n, c.max_seq);
+    for (int i = 0; i < n; ++i)
+        CW_CHECK_ARG(tokens[i] < (uint32_t)c.vocab, "cw_model_prefill: tokens[%d]=%u >= vocab", i,
+                     tokens[i]);
+    CW_HIP(hipMemcpy(m->prompt_dev, tokens, (size_t)n * 4, hipMemcpyHostToDevice));
+    const bool batched = c.kv_dtype == CW_F16 && c.head_dim == 128;
+    if (batched) {
+        CW_TRY(ensure_prefill(m, n));
+        CW_TRY(enqueue_prefill(m, n, start_pos));
+        // the last position's logits (the prompt phase discards the others,
+        // mod.rs:93-103) and the final-normed hidden state
+        const float *last = m->pf_hidden + (size_t)(n - 1) * c.dim;
+        GemvArgs g{};
+        g.x = last;
+        g.norm_w = m->final_norm;
+        g.eps = c.eps;
+        g.sA = m->lm_head.s;
+        g.qA = m->lm_head.q;
+        g.y = m->logits;
+        g.K = c.dim;
+        g.N = c.vocab;
+        CW_TRY(launch_q4_gemv(m->ctx, XS_RMSNORM, EPI_STORE, g));
+        CW_TRY(launch_argmax(m->ctx, m->logits, c.vocab, m->argmax_out, m->argmax_scratch,
+                             nullptr, nullptr, nullptr));
+        CW_TRY(launch_rmsnorm(m->ctx, last, m->final_norm, 1, c.dim, c.eps, m->hidden_out));
+    } else {
+        // head_dim other than 128 or an f32 cache: the per-token step, n times
+        GenState s{start_pos, tokens[0], start_pos, n, 0, 0};
+        CW_TRY(set_state(m, s));
+        CW_TRY(run_steps(m, n, CW_STEP_EAGER));
+        CW_TRY(launch_rmsnorm(m->ctx, m->hidden, m->final_norm, 1, c.dim, c.eps, m->hidden_out));
+    }
+    uint32_t r = 0;
+    CW_HIP(hipMemcpyAsync(&r, m->argmax_out, 4, hipMemcpyDeviceToHost, m->ctx->stream));
+    CW_HIP(hipStreamSynchronize(m->ctx->stream));
+    if (next_token) *next_token = r;
+    // decoding continues at start_pos + n with the predicted token
+    GenState s{start_pos + n, r, start_pos + n, 1, 0, c.max_seq};
+    return set_state(m, s);
 }
 
 int cw_model_reset_state(cw_model *m, uint32_t token, int pos) {

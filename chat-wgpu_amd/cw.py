@@ -65,6 +65,7 @@ _SIGS = {
     "cw_q4_gemv": (_I, [_P, _P, _P, _P, _I, _I, _P]),
     "cw_q4_gemv_add": (_I, [_P, _P, _P, _P, _I, _I, _P, _P]),
     "cw_q4_gemv_swiglu": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _P]),
+    "cw_q4_gemm": (_I, [_P, _P, _I, _P, _P, _I, _I, _P]),
     "cw_rmsnorm": (_I, [_P, _P, _P, _I, _I, _F, _P]),
     "cw_rope": (_I, [_P, _P, _I, _I, _I, _F, _P]),
     "cw_attention": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
@@ -94,6 +95,7 @@ _SIGS = {
     "cw_generate": (_I, [_P, _P, _I, _I, _I, _I, _P]),
     "cw_model_decode_async": (_I, [_P, _I, _I]),
     "cw_model_reset_state": (_I, [_P, _U32, _I]),
+    "cw_model_prefill": (_I, [_P, _P, _I, _I, C.POINTER(_U32)]),
     "cw_model_tokens": (_I, [_P, _P, _I, C.POINTER(_I)]),
     "cw_model_profile_step": (_I, [_P, _P, _I, C.POINTER(_I), C.POINTER(C.c_double)]),
     "cw_profile_begin": (_I, [_P]),
@@ -279,6 +281,11 @@ class Context:
                                       out_f, y.ptr))
         return y
 
+    def q4_gemm(self, x, m, scales, quants, in_f, out_f, y=None):
+        y = y if y is not None else self.empty((m, out_f))
+        check(lib().cw_q4_gemm(self.h, x.ptr, m, scales.ptr, quants.ptr, in_f, out_f, y.ptr))
+        return y
+
     def rmsnorm(self, x, w, rows, dim, eps):
         y = self.empty(rows * dim)
         check(lib().cw_rmsnorm(self.h, x.ptr, w.ptr, rows, dim, eps, y.ptr))
@@ -420,6 +427,13 @@ class Model:
         check(lib().cw_generate(self.h, _ptr(prompt), len(prompt), max_new, start_pos,
                                 int(mode), _ptr(out)))
         return out
+
+    def prefill(self, tokens, start_pos=0):
+        """Batched prompt phase; returns the argmax of the last position."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+        nxt = _U32(0)
+        check(lib().cw_model_prefill(self.h, _ptr(tokens), len(tokens), start_pos, C.byref(nxt)))
+        return int(nxt.value)
 
     def reset_state(self, token, pos):
         check(lib().cw_model_reset_state(self.h, int(token), int(pos)))

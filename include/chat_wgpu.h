@@ -126,6 +126,13 @@ int cw_embed(cw_ctx *ctx, const float *table, int vocab, int dim, const uint32_t
  * word per workgroup to out_dev.  Time it with the profiler or events. */
 int cw_hbm_read_probe(cw_ctx *ctx, const void *buf, size_t bytes, int blocks, uint32_t *out_dev);
 
+/* Batched form of q4::gemv (src/kernels/q4.rs:9-30): y[m][out_f] = x[m][in_f]
+ * . W^T for m rows at once, on the matrix cores (the reference has no batched
+ * path; every row equals cw_q4_gemv of that row to within 1e-4 relative).
+ * x and y device f32, row-major; quants 8-byte aligned. */
+int cw_q4_gemm(cw_ctx *ctx, const float *x, int m, const uint16_t *scales, const uint8_t *quants,
+               int in_f, int out_f, float *y);
+
 /* ---------------------------------------------------------------- */
 /* Host-side Q4 helpers                                              */
 /* ---------------------------------------------------------------- */
@@ -228,6 +235,16 @@ int cw_model_decode_async(cw_model *m, int n_steps, int mode);
  * staging, after compute (20L+8 stamps in all); *tick_hz is the clock rate. */
 int cw_model_profile_step(cw_model *m, int64_t *ticks, int max_n, int *n_out, double *tick_hz);
 /* Reset the decode state to (token, pos) without touching the cache. */
+/* The prompt phase of model::generate (src/model/mod.rs:57-125: P forwards,
+ * the logits of all but the last discarded) for n tokens at positions
+ * start_pos..start_pos+n-1, batched: each layer runs as Q4_0 GEMMs on the
+ * matrix cores and causal attention over the cache (f16 cache and head_dim
+ * 128; other configurations run the per-token step n times).  Writes the KV
+ * rows, leaves the last position's logits (cw_model_logits) and final-normed
+ * hidden state (cw_model_hidden), returns its argmax in *next_token, and sets
+ * the decode state to (next_token, start_pos + n). */
+int cw_model_prefill(cw_model *m, const uint32_t *tokens, int n, int start_pos,
+                     uint32_t *next_token);
 int cw_model_reset_state(cw_model *m, uint32_t token, int pos);
 /* Download the tokens produced so far by the device-resident loop. */
 int cw_model_tokens(cw_model *m, uint32_t *host_out, int max_n, int *n_out);
