@@ -103,6 +103,48 @@ def cpu_baseline_8b(cfg, weights, k, v, start_tok, budget_s):
     return n / el, n, el
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 matrix peak
+
+
+def bench_prefill_8b(ctx, m, cfg, P=512, reps=3):
+    """Batched prefill of a P-token prompt (uniform ids) on the 8B model:
+    wall time of cw_model_prefill (synchronous), the linear-layer flops
+    (2 P sum(N K) over the 36 layers; the LM head runs for the last position
+    only) and the causal attention flops, and a per-kernel profile of one
+    prefill."""
+    prompt = cw.synth_tokens(cw.synth_key(8008, "prefill"), P, cfg.vocab)
+    m.prefill(prompt)  # allocates the batched buffers
+    ctx.flush()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        m.prefill(prompt)
+        ts.append(time.perf_counter() - t0)
+    el = min(ts)
+    ctx.profile_begin()
+    m.prefill(prompt)
+    prof = {}
+    for name, c, ms in ctx.profile_report():
+        prof[name] = prof.get(name, 0.0) + ms
+    q, kv = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+    d, h = cfg.dim, cfg.hidden
+    lin = 2.0 * P * cfg.n_layers * ((q + 2 * kv) * d + d * q + 2 * h * d + d * h)
+    att = 2.0 * 2.0 * cfg.n_heads * cfg.head_dim * (P * (P + 1) / 2) * cfg.n_layers
+    gemm_ms = sum(v for k, v in prof.items() if k.startswith("q4_gemm"))
+    return {
+        "workload": f"qwen3-8b-shape batched prefill, {P}-token uniform prompt from position 0, "
+                    "f16 KV, logits of the last position",
+        "tok_s": round(P / el, 1), "ms": round(el * 1e3, 3),
+        "linear_tflop": round(lin / 1e12, 3), "attention_gflop": round(att / 1e9, 2),
+        "gemm_ms": round(gemm_ms, 3),
+        "mfma_util": round(lin / (gemm_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+        "mfma_util_note": "useful linear flops / GEMM kernel time / 2.5 PFLOP/s dense bf16; "
+                          "each Q4 block issues two MFMAs (activation hi and lo halves, for "
+                          "f32-level parity), so the matrix pipes run twice the useful flops",
+        "kernel_ms": {k: round(v, 3) for k, v in prof.items()},
+    }
+
+
 def gemv_profile(prof, n_steps):
     """(ms per token, launches per token) of the q4_gemv labels of a profile."""
     g = [(c, ms) for name, c, ms in prof if name.startswith("q4_gemv")]
@@ -342,6 +384,9 @@ def main():
                                             f"position 4096 on the C oracle ({cel:.1f}s); "
                                             f"host {model_name}, {ncpu} cpus"}
     del weights
+    if not args.no_extras:
+        log("prefill (512 tokens, batched) ...")
+        result["extras"]["qwen3_8b_prefill_512"] = bench_prefill_8b(ctx, m, cfg)
     m.close()
 
     if not args.no_extras:
