@@ -83,47 +83,26 @@ __global__ __launch_bounds__(kT) void split_rows_kernel(const float *__restrict_
 // ---------------------------------------------------------------------------
 // Q4_0 dequant-GEMM: y[M][N] = x[M][K] . W[N][K]^T (W split GGUF Q4_0).
 //
-// Workgroup tile 64 x 64, four waves of 32 x 32 (2 x 2 MFMA tiles).  Per
-// 32-wide block a wave loads its A operands (2 row tiles x hi/lo, 16 B per
-// lane) and B operands (2 column tiles, the 8 quant bytes that hold its 8
-// nibbles, plus the block scale) straight from memory, PD blocks ahead;
-// the loop body is branch-free (block index clamped, blocks past the end
-// weighted 0).  Epilogues: store, residual add, SwiGLU of a gate/up pair.
+// Workgroup tile 128 (rows of x) x 64 (rows of W), four waves of 64 x 32
+// (4 x 2 MFMA tiles of 16 x 16).  Per 32-wide Q4 block the workgroup stages
+// in LDS, double-buffered: the x tile as bf16 hi and lo, and the W tile
+// dequantized once to bf16 (q - 8) with its f32 block scales.  While the
+// waves run the block's MFMAs from one buffer, the next block's global loads
+// are in flight into registers; they are written (and W dequantized) into the
+// other buffer, then one barrier.  LDS rows are padded by 16 B so the 16 lanes
+// of a fragment read hit 16 disjoint bank quads.
+constexpr int kBM = 128, kBN = 64;
+constexpr int kRowB = 64 + 16;  // bytes per LDS row: 32 bf16 + pad
+constexpr int kStageA = kBM * kRowB;          // one of x hi / x lo
+constexpr int kStageB = kBN * kRowB;          // W (q - 8)
+constexpr int kStage = 2 * kStageA + kStageB; // + scales (f32) after
 
-constexpr int kPD = 3;  // ring slots: blocks of operands loaded ahead of use
-
-struct Ops {
-    uint4 ah[2], al[2];  // A hi/lo per row tile
-    uint2 bq[2][2];      // quant bytes per column tile (per matrix)
-    uint32_t bd[2][2];   // f16 scale bits per column tile (per matrix)
-};
-
-template <int NM>
-__device__ __forceinline__ void load_ops(const cwi::GemmArgs &a, int nb, int b, const int (&ra)[2],
-                                         const int (&cb)[2], int lg, Ops &o) {
-    const int bc = b < nb ? b : nb - 1;
-    const size_t ko = (size_t)bc * 32 + 8 * lg;
-#pragma unroll
-    for (int mi = 0; mi < 2; ++mi) {
-        o.ah[mi] = *reinterpret_cast<const uint4 *>(a.xhi + (size_t)ra[mi] * a.K + ko);
-        o.al[mi] = *reinterpret_cast<const uint4 *>(a.xlo + (size_t)ra[mi] * a.K + ko);
-    }
-#pragma unroll
-    for (int w = 0; w < NM; ++w) {
-        const uint8_t *q = w ? a.qB : a.qA;
-        const uint16_t *s = w ? a.sB : a.sA;
-#pragma unroll
-        for (int ni = 0; ni < 2; ++ni) {
-            const size_t blk = (size_t)cb[ni] * nb + bc;
-            o.bq[w][ni] = *reinterpret_cast<const uint2 *>(q + blk * 16 + 8 * (lg & 1));
-            const uint32_t d = s[blk];
-            o.bd[w][ni] = b < nb ? d : 0u;  // f16 +0: blocks past the end add nothing
-        }
-    }
+__device__ __forceinline__ float f16_bits_val(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
 // 8 nibbles (low or high halves of 8 quant bytes) -> bf16 (q - 8), exact
-__device__ __forceinline__ bf16x8 dequant8(uint2 q, bool high) {
+__device__ __forceinline__ uint4 dequant8(uint2 q, bool high) {
     uint32_t w0 = q.x, w1 = q.y;
     if (high) {
         w0 >>= 4;
@@ -143,83 +122,133 @@ __device__ __forceinline__ bf16x8 dequant8(uint2 q, bool high) {
         p[2 * h + 1] = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f3),
                                              __builtin_bit_cast(uint32_t, f2), 0x07060302u);
     }
-    return __builtin_bit_cast(bf16x8, make_uint4(p[0], p[1], p[2], p[3]));
+    return make_uint4(p[0], p[1], p[2], p[3]);
 }
 
-__device__ __forceinline__ float f16_bits_val(uint32_t h) {
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+// Global loads of one block into registers: thread t brings 4 x 16 B of x
+// (hi rows t/2.., lo) and, for t < NM * 64, the 16 quant bytes and the scale
+// of one W row.
+template <int NM>
+struct Stage {
+    uint4 x[4];
+    uint4 q;
+    uint32_t d;
+};
+
+template <int NM>
+__device__ __forceinline__ void stage_load(const cwi::GemmArgs &a, int nb, int b, int m0, int n0,
+                                           int tid, Stage<NM> &st) {
+    const int bc = b < nb ? b : nb - 1;
+    // x: 128 rows x 64 B (hi) + 128 x 64 B (lo) = 1024 units of 16 B
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int f = tid + u * kT;             // 0..1023
+        const int half = f >> 9;                // 0: hi, 1: lo
+        const int row = (f >> 2) & (kBM - 1), c = f & 3;
+        const int m = min(m0 + row, a.M - 1);
+        const uint16_t *src = half ? a.xlo : a.xhi;
+        st.x[u] = *reinterpret_cast<const uint4 *>(src + (size_t)m * a.K + (size_t)bc * 32 + c * 8);
+    }
+    if (tid < NM * kBN) {
+        const int w = tid >> 6, col = tid & (kBN - 1);
+        const int n = min(n0 + col, a.N - 1);
+        const uint8_t *q = w ? a.qB : a.qA;
+        const uint16_t *s = w ? a.sB : a.sA;
+        const size_t blk = (size_t)n * nb + bc;
+        st.q = *reinterpret_cast<const uint4 *>(q + blk * 16);
+        st.d = s[blk];
+    }
+}
+
+template <int NM>
+__device__ __forceinline__ void stage_store(const Stage<NM> &st, unsigned char *buf, int tid) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int f = tid + u * kT;
+        const int half = f >> 9;
+        const int row = (f >> 2) & (kBM - 1), c = f & 3;
+        *reinterpret_cast<uint4 *>(buf + half * kStageA + row * kRowB + c * 16) = st.x[u];
+    }
+    if (tid < NM * kBN) {
+        const int w = tid >> 6, col = tid & (kBN - 1);
+        unsigned char *wb = buf + 2 * kStageA + w * (kStageB + kBN * 4);
+        // elements 0..15: low nibbles of bytes 0..15; 16..31: high nibbles
+        const uint2 lo8 = make_uint2(st.q.x, st.q.y), hi8 = make_uint2(st.q.z, st.q.w);
+        *reinterpret_cast<uint4 *>(wb + col * kRowB + 0) = dequant8(lo8, false);
+        *reinterpret_cast<uint4 *>(wb + col * kRowB + 16) = dequant8(hi8, false);
+        *reinterpret_cast<uint4 *>(wb + col * kRowB + 32) = dequant8(lo8, true);
+        *reinterpret_cast<uint4 *>(wb + col * kRowB + 48) = dequant8(hi8, true);
+        reinterpret_cast<float *>(wb + kStageB)[col] = f16_bits_val(st.d);
+    }
 }
 
 template <int EPI>
 __global__ __launch_bounds__(kT) void q4_gemm_kernel(cwi::GemmArgs a) {
     constexpr int NM = EPI == cwi::EPI_SWIGLU ? 2 : 1;  // weight matrices
+    constexpr int kBuf = 2 * kStageA + NM * (kStageB + kBN * 4);
+    __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kBuf];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 15, lg = lane >> 4;
-    const int wm = blockIdx.y * 64 + (wave >> 1) * 32;
-    const int wn = blockIdx.x * 64 + (wave & 1) * 32;
+    const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+    const int wr = (wave >> 1) * 64, wc = (wave & 1) * 32;  // wave tile within the block tile
     const int nb = a.K >> 5;
-    int ra[2], cb[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        ra[i] = min(wm + i * 16 + li, a.M - 1);
-        cb[i] = min(wn + i * 16 + li, a.N - 1);
-    }
-    f32x4 acc[NM][2][2];
+
+    f32x4 acc[NM][4][2];
 #pragma unroll
     for (int w = 0; w < NM; ++w)
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
+        for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni) acc[w][mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    Ops ring[kPD];
+    Stage<NM> st;
+    stage_load<NM>(a, nb, 0, m0, n0, tid, st);
+    stage_store<NM>(st, lds, tid);
+    __syncthreads();
+    for (int b = 0; b < nb; ++b) {
+        const unsigned char *cur = lds + (b & 1) * kBuf;
+        stage_load<NM>(a, nb, b + 1, m0, n0, tid, st);  // past the end: a clamped re-load
+        // fragments: A rows wr + 16 mi + li, k 8 lg..; B columns wc + 16 ni + li
+        bf16x8 A[4][2];
 #pragma unroll
-    for (int u = 0; u < kPD; ++u) load_ops<NM>(a, nb, u, ra, cb, lg, ring[u]);
-    const bool high = lg >= 2;
-    for (int b0 = 0; b0 < nb; b0 += kPD) {
+        for (int mi = 0; mi < 4; ++mi) {
+            const int row = wr + 16 * mi + li;
+            A[mi][0] = *reinterpret_cast<const bf16x8 *>(cur + row * kRowB + lg * 16);
+            A[mi][1] = *reinterpret_cast<const bf16x8 *>(cur + kStageA + row * kRowB + lg * 16);
+        }
 #pragma unroll
-        for (int u = 0; u < kPD; ++u) {
-            const Ops &o = ring[u];
-            bf16x8 A[2][2];
+        for (int w = 0; w < NM; ++w) {
+            const unsigned char *wb = cur + 2 * kStageA + w * (kStageB + kBN * 4);
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi) {
-                A[mi][0] = __builtin_bit_cast(bf16x8, o.ah[mi]);
-                A[mi][1] = __builtin_bit_cast(bf16x8, o.al[mi]);
-            }
+            for (int ni = 0; ni < 2; ++ni) {
+                const int col = wc + 16 * ni + li;
+                const bf16x8 B = *reinterpret_cast<const bf16x8 *>(wb + col * kRowB + lg * 16);
+                const float d = reinterpret_cast<const float *>(wb + kStageB)[col];
 #pragma unroll
-            for (int w = 0; w < NM; ++w) {
+                for (int mi = 0; mi < 4; ++mi) {
+                    f32x4 t = f32x4{0.f, 0.f, 0.f, 0.f};
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mi][0], B, t, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mi][1], B, t, 0, 0, 0);
 #pragma unroll
-                for (int ni = 0; ni < 2; ++ni) {
-                    const bf16x8 B = dequant8(o.bq[w][ni], high);
-                    const float d = f16_bits_val(o.bd[w][ni]);
-#pragma unroll
-                    for (int mi = 0; mi < 2; ++mi) {
-                        f32x4 t = f32x4{0.f, 0.f, 0.f, 0.f};
-                        t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mi][0], B, t, 0, 0, 0);
-                        t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mi][1], B, t, 0, 0, 0);
-#pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            acc[w][mi][ni][r] = __builtin_fmaf(d, t[r], acc[w][mi][ni][r]);
-                    }
+                    for (int r = 0; r < 4; ++r)
+                        acc[w][mi][ni][r] = __builtin_fmaf(d, t[r], acc[w][mi][ni][r]);
                 }
             }
-            // reload the slot after its last use, so the loads land in its own
-            // registers (no copies that would wait on them)
-            __builtin_amdgcn_sched_barrier(0);
-            load_ops<NM>(a, nb, b0 + u + kPD, ra, cb, lg, ring[u]);
         }
+        stage_store<NM>(st, lds + ((b + 1) & 1) * kBuf, tid);
+        __syncthreads();
     }
 
     // lane holds rows 4 lg + r of each row tile, column li of each column tile
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
+    for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni) {
-            const int n = wn + ni * 16 + li;
+            const int n = n0 + wc + ni * 16 + li;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int m = wm + mi * 16 + 4 * lg + r;
+                const int m = m0 + wr + mi * 16 + 4 * lg + r;
                 if (m < a.M && n < a.N) {
                     const size_t o = (size_t)m * a.N + n;
                     const float v = acc[0][mi][ni][r];
@@ -495,7 +524,7 @@ int launch_split_rows(cw_ctx *ctx, const float *x, const float *norm_w, float ep
 }
 
 int launch_q4_gemm(cw_ctx *ctx, Epi epi, const GemmArgs &a) {
-    const dim3 grid((a.N + 63) / 64, (a.M + 63) / 64);
+    const dim3 grid((a.N + kBN - 1) / kBN, (a.M + kBM - 1) / kBM);
     switch (epi) {
         case EPI_STORE:
             return launch(ctx, "q4_gemm", q4_gemm_kernel<EPI_STORE>, grid, dim3(kT), 0, a);
@@ -536,8 +565,8 @@ extern "C" int cw_q4_gemm(cw_ctx *ctx, const float *x, int m, const uint16_t *sc
     CW_CHECK_ARG(in_f > 0 && in_f % 32 == 0, "cw_q4_gemm: in_f=%d must be a positive multiple of 32",
                  in_f);
     CW_CHECK_ARG(out_f > 0, "cw_q4_gemm: out_f=%d must be positive", out_f);
-    CW_CHECK_ARG(((uintptr_t)quants & 7) == 0 && ((uintptr_t)scales & 1) == 0,
-                 "cw_q4_gemm: quants must be 8-byte and scales 2-byte aligned");
+    CW_CHECK_ARG(((uintptr_t)quants & 15) == 0 && ((uintptr_t)scales & 1) == 0,
+                 "cw_q4_gemm: quants must be 16-byte and scales 2-byte aligned");
     void *scratch = nullptr;
     const size_t n = (size_t)m * in_f;
     CW_TRY(ctx_scratch(ctx, n * 4, &scratch));

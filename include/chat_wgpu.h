@@ -129,7 +129,7 @@ int cw_hbm_read_probe(cw_ctx *ctx, const void *buf, size_t bytes, int blocks, ui
 /* Batched form of q4::gemv (src/kernels/q4.rs:9-30): y[m][out_f] = x[m][in_f]
  * . W^T for m rows at once, on the matrix cores (the reference has no batched
  * path; every row equals cw_q4_gemv of that row to within 1e-4 relative).
- * x and y device f32, row-major; quants 8-byte aligned. */
+ * x and y device f32, row-major; quants 16-byte aligned. */
 int cw_q4_gemm(cw_ctx *ctx, const float *x, int m, const uint16_t *scales, const uint8_t *quants,
                int in_f, int out_f, float *y);
 
