@@ -17,7 +17,7 @@ LIB = os.path.join(PKG, "libchatwgpu.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["context.hip", "q4_gemv.hip", "ops.hip", "attention.hip", "decode_step.hip", "prefill.hip",
-           "host_utils.cpp", "model.cpp"]
+           "host_utils.cpp", "gguf.cpp", "model.cpp"]
 
 # No packed FP32 (v_pk_*_f32): some forms have produced wrong results on these boxes.
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",

@@ -4,9 +4,11 @@
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdint>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "chat_wgpu.h"
@@ -15,6 +17,28 @@ namespace cwi {
 
 void set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
 int hip_fail(hipError_t e, const char *what, const char *file, int line);
+
+// Run f(lo, hi) over [0, n) split across up to 16 host threads (one thread
+// below 64 Ki items).  Each item's result depends only on the item, so the
+// split never changes the output.
+template <class F>
+void parallel_for(size_t n, F f) {
+    unsigned hw = std::thread::hardware_concurrency();
+    if (hw == 0) hw = 1;
+    const size_t nt = std::min<size_t>(std::min<size_t>(hw, 16), n / 65536 + 1);
+    if (nt <= 1) {
+        f((size_t)0, n);
+        return;
+    }
+    std::vector<std::thread> ts;
+    const size_t step = (n + nt - 1) / nt;
+    for (size_t t = 0; t < nt; ++t) {
+        const size_t lo = t * step, hi = std::min(n, lo + step);
+        if (lo >= hi) break;
+        ts.emplace_back([=] { f(lo, hi); });
+    }
+    for (auto &t : ts) t.join();
+}
 
 }  // namespace cwi
 

@@ -8,7 +8,6 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
-#include <thread>
 #include <vector>
 
 #include "cw_internal.hpp"
@@ -29,25 +28,6 @@ inline double normal01(uint64_t key, uint64_t i) {
     const double u1 = (double)((h1 >> 11) + 1) * 0x1p-53;  // (0, 1]
     const double u2 = (double)(h2 >> 11) * 0x1p-53;        // [0, 1)
     return std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2);
-}
-
-template <class F>
-void parallel_for(size_t n, F f) {
-    unsigned hw = std::thread::hardware_concurrency();
-    if (hw == 0) hw = 1;
-    size_t nt = std::min<size_t>(std::min<size_t>(hw, 16), n / 65536 + 1);
-    if (nt <= 1) {
-        f((size_t)0, n);
-        return;
-    }
-    std::vector<std::thread> ts;
-    const size_t step = (n + nt - 1) / nt;
-    for (size_t t = 0; t < nt; ++t) {
-        const size_t lo = t * step, hi = std::min(n, lo + step);
-        if (lo >= hi) break;
-        ts.emplace_back([=] { f(lo, hi); });
-    }
-    for (auto &t : ts) t.join();
 }
 
 // Rust f32::max (NaN operand ignored) and `f32 as i32` (saturating, NaN->0).
@@ -73,7 +53,7 @@ int cw_q4_quantize(const float *data, size_t out_f, size_t in_f, uint16_t *scale
     CW_CHECK_ARG(in_f > 0 && in_f % 32 == 0, "cw_q4_quantize: in_f=%zu must be a multiple of 32",
                  in_f);
     const size_t nb = in_f / 32;
-    parallel_for(out_f, [&](size_t lo, size_t hi) {
+    cwi::parallel_for(out_f, [&](size_t lo, size_t hi) {
         for (size_t o = lo; o < hi; ++o) {
             for (size_t b = 0; b < nb; ++b) {
                 const float *v = data + o * in_f + b * 32;
@@ -117,7 +97,7 @@ uint64_t cw_synth_key(uint64_t seed, const char *name) {
 int cw_synth_q4(uint64_t key, size_t nblocks, float sigma, uint16_t *scales, uint8_t *quants) {
     CW_CHECK_ARG(scales && quants, "cw_synth_q4: null argument");
     const uint64_t kd = mix64(key ^ 0xD5ull), kq = mix64(key ^ 0x95ull);
-    parallel_for(nblocks, [&](size_t lo, size_t hi) {
+    cwi::parallel_for(nblocks, [&](size_t lo, size_t hi) {
         for (size_t b = lo; b < hi; ++b) {
             const float d = (float)std::fabs((double)sigma * normal01(kd, b));
             scales[b] = cwi::f32_to_f16_bits(d);
@@ -131,7 +111,7 @@ int cw_synth_q4(uint64_t key, size_t nblocks, float sigma, uint16_t *scales, uin
 
 int cw_synth_normal_f32(uint64_t key, size_t n, float mean, float std_, float *out) {
     CW_CHECK_ARG(out != nullptr, "cw_synth_normal_f32: null argument");
-    parallel_for(n, [&](size_t lo, size_t hi) {
+    cwi::parallel_for(n, [&](size_t lo, size_t hi) {
         for (size_t i = lo; i < hi; ++i)
             out[i] = (float)((double)mean + (double)std_ * normal01(key, i));
     });
@@ -140,7 +120,7 @@ int cw_synth_normal_f32(uint64_t key, size_t n, float mean, float std_, float *o
 
 int cw_synth_normal_f16(uint64_t key, size_t n, float mean, float std_, uint16_t *out) {
     CW_CHECK_ARG(out != nullptr, "cw_synth_normal_f16: null argument");
-    parallel_for(n, [&](size_t lo, size_t hi) {
+    cwi::parallel_for(n, [&](size_t lo, size_t hi) {
         for (size_t i = lo; i < hi; ++i)
             out[i] = cwi::f32_to_f16_bits((float)((double)mean + (double)std_ * normal01(key, i)));
     });

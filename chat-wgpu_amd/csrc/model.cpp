@@ -655,6 +655,47 @@ int cw_model_load_synthetic(cw_model *m, uint64_t seed) {
     return CW_OK;
 }
 
+int cw_model_load_gguf(cw_model *m, const cw_gguf *g) {
+    CW_CHECK_ARG(m && g, "cw_model_load_gguf: null argument");
+    const auto &c = m->cfg;
+    std::vector<uint16_t> s;
+    std::vector<uint8_t> q;
+    std::vector<float> f;
+    char name[96];
+    for (int i = 0; i < c.n_layers; ++i) {
+        for (int id = 0; id < T_N; ++id) {
+            snprintf(name, sizeof name, "blk.%d.%s.weight", i, kLayerNames[id]);
+            if (id < T_Q) {
+                f.resize((id == T_Q_NORM || id == T_K_NORM) ? c.head_dim : c.dim);
+                CW_TRY(cw_gguf_tensor_f32(g, name, f.data(), f.size()));
+                CW_TRY(cw_model_set_f32(m, name, f.data()));
+            } else {
+                int out_f = 0, in_f = 0;
+                proj_shape(m, id, &out_f, &in_f);
+                const size_t nblk = (size_t)out_f * (in_f / 32);
+                s.resize(nblk);
+                q.resize(nblk * 16);
+                CW_TRY(cw_gguf_tensor_q4(g, name, out_f, in_f, s.data(), q.data()));
+                CW_TRY(cw_model_set_q4(m, name, s.data(), q.data()));
+            }
+        }
+    }
+    f.resize(c.dim);
+    CW_TRY(cw_gguf_tensor_f32(g, "output_norm.weight", f.data(), f.size()));
+    CW_TRY(cw_model_set_f32(m, "output_norm.weight", f.data()));
+    f.resize((size_t)c.vocab * c.dim);
+    CW_TRY(cw_gguf_tensor_f32(g, "token_embd.weight", f.data(), f.size()));
+    CW_TRY(cw_model_set_f32(m, "token_embd.weight", f.data()));
+    if (cw_gguf_has(g, "output.weight")) {
+        const size_t nblk = (size_t)c.vocab * (c.dim / 32);
+        s.resize(nblk);
+        q.resize(nblk * 16);
+        CW_TRY(cw_gguf_tensor_q4(g, "output.weight", c.vocab, c.dim, s.data(), q.data()));
+        CW_TRY(cw_model_set_q4(m, "output.weight", s.data(), q.data()));
+    }
+    return CW_OK;
+}
+
 int cw_model_finalize(cw_model *m) {
     CW_CHECK_ARG(m != nullptr, "cw_model_finalize: null model");
     const auto &c = m->cfg;

@@ -98,6 +98,22 @@ _SIGS = {
     "cw_model_prefill": (_I, [_P, _P, _I, _I, C.POINTER(_U32)]),
     "cw_model_tokens": (_I, [_P, _P, _I, C.POINTER(_I)]),
     "cw_model_profile_step": (_I, [_P, _P, _I, C.POINTER(_I), C.POINTER(C.c_double)]),
+    "cw_gguf_open": (_I, [C.c_char_p, C.POINTER(_P)]),
+    "cw_gguf_parse": (_I, [_P, _SZ, C.POINTER(_P)]),
+    "cw_gguf_close": (_I, [_P]),
+    "cw_gguf_info": (_I, [_P, C.POINTER(_U32), C.POINTER(_U64), C.POINTER(_U64),
+                          C.POINTER(_U64)]),
+    "cw_gguf_meta_u32": (_I, [_P, C.c_char_p, C.POINTER(_U32)]),
+    "cw_gguf_meta_f32": (_I, [_P, C.c_char_p, C.POINTER(_F)]),
+    "cw_gguf_meta_str": (_I, [_P, C.c_char_p, C.c_char_p, _SZ, C.POINTER(_SZ)]),
+    "cw_gguf_has": (_I, [_P, C.c_char_p]),
+    "cw_gguf_tensor_name": (_I, [_P, _U64, C.c_char_p, _SZ]),
+    "cw_gguf_tensor_info": (_I, [_P, C.c_char_p, C.POINTER(_U32), C.POINTER(_I),
+                                 C.POINTER(_U64), _I, C.POINTER(_U64), C.POINTER(_U64)]),
+    "cw_gguf_tensor_f32": (_I, [_P, C.c_char_p, _P, _SZ]),
+    "cw_gguf_tensor_q4": (_I, [_P, C.c_char_p, _SZ, _SZ, _P, _P]),
+    "cw_gguf_model_config": (_I, [_P, _I, _I, C.POINTER(ModelConfig)]),
+    "cw_model_load_gguf": (_I, [_P, _P]),
     "cw_profile_begin": (_I, [_P]),
     "cw_profile_report": (_I, [_P, C.c_char_p, _SZ]),
 }
@@ -181,6 +197,97 @@ def synth_tokens(key, n, vocab):
     out = np.empty(n, np.uint32)
     check(lib().cw_synth_tokens(key, n, vocab, _ptr(out)))
     return out
+
+
+# ---------------------------------------------------------------- GGUF container
+
+GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q4_1, GGML_Q8_0, GGML_Q6_K = 0, 1, 2, 3, 8, 14
+
+
+class Gguf:
+    """GgufWeights (src/loader/gguf.rs): a parsed GGUF container, memory-mapped
+    (`Gguf(path)`) or copied from bytes (`Gguf(data=b"...")`), with the
+    Weights accessors meta_u32 / meta_f32 / has / tensor_f32 (= matrix_raw,
+    vector_data) and the split Q4_0 repack tensor_q4."""
+
+    def __init__(self, path=None, data=None):
+        h = _P()
+        if path is not None:
+            check(lib().cw_gguf_open(os.fsencode(path), C.byref(h)))
+        else:
+            buf = bytes(data)
+            check(lib().cw_gguf_parse(buf, len(buf), C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().cw_gguf_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def info(self):
+        v, nt, nm, off = _U32(), _U64(), _U64(), _U64()
+        check(lib().cw_gguf_info(self.h, C.byref(v), C.byref(nt), C.byref(nm), C.byref(off)))
+        return {"version": v.value, "n_tensors": nt.value, "n_meta": nm.value,
+                "data_offset": off.value}
+
+    def meta_u32(self, key):
+        r = _U32()
+        check(lib().cw_gguf_meta_u32(self.h, key.encode(), C.byref(r)))
+        return r.value
+
+    def meta_f32(self, key):
+        r = _F()
+        check(lib().cw_gguf_meta_f32(self.h, key.encode(), C.byref(r)))
+        return r.value
+
+    def meta_str(self, key):
+        n = _SZ()
+        check(lib().cw_gguf_meta_str(self.h, key.encode(), None, 0, C.byref(n)))
+        buf = C.create_string_buffer(n.value + 1)
+        check(lib().cw_gguf_meta_str(self.h, key.encode(), buf, len(buf), None))
+        return buf.raw[:n.value]
+
+    def has(self, name):
+        return bool(lib().cw_gguf_has(self.h, name.encode()))
+
+    def names(self):
+        out = []
+        buf = C.create_string_buffer(4096)
+        for i in range(self.info()["n_tensors"]):
+            check(lib().cw_gguf_tensor_name(self.h, i, buf, len(buf)))
+            out.append(buf.value.decode())
+        return out
+
+    def tensor_info(self, name):
+        dt, nd, ne, off = _U32(), _I(), _U64(), _U64()
+        dims = (_U64 * 16)()
+        check(lib().cw_gguf_tensor_info(self.h, name.encode(), C.byref(dt), C.byref(nd), dims,
+                                        16, C.byref(ne), C.byref(off)))
+        return {"dtype": dt.value, "dims": list(dims[:nd.value]), "n_elems": ne.value,
+                "offset": off.value}
+
+    def tensor_f32(self, name):
+        n = self.tensor_info(name)["n_elems"]
+        out = np.empty(n, np.float32)
+        check(lib().cw_gguf_tensor_f32(self.h, name.encode(), _ptr(out), n))
+        return out
+
+    def tensor_q4(self, name, out_f, in_f):
+        s = np.empty((out_f, in_f // 32), np.uint16)
+        q = np.empty((out_f, in_f // 32, 16), np.uint8)
+        check(lib().cw_gguf_tensor_q4(self.h, name.encode(), out_f, in_f, _ptr(s), _ptr(q)))
+        return s, q
+
+    def model_config(self, max_seq, kv_dtype=CW_F16):
+        cfg = ModelConfig()
+        check(lib().cw_gguf_model_config(self.h, max_seq, kv_dtype, C.byref(cfg)))
+        return cfg
 
 
 # ---------------------------------------------------------------- device context
@@ -397,6 +504,10 @@ class Model:
 
     def load_synthetic(self, seed):
         check(lib().cw_model_load_synthetic(self.h, seed))
+
+    def load_gguf(self, g):
+        """Every tensor of a Gguf (Qwen3::load's walk, qwen3.rs:56-100)."""
+        check(lib().cw_model_load_gguf(self.h, g.h))
 
     def finalize(self):
         check(lib().cw_model_finalize(self.h))

@@ -29,6 +29,8 @@ extern "C" {
 #define CW_ERR_HIP (-2)     /* a HIP runtime call failed */
 #define CW_ERR_OOM (-3)     /* device or host allocation failed */
 #define CW_ERR_STATE (-4)   /* call not valid in the current state */
+#define CW_ERR_FORMAT (-5)  /* malformed or unsupported file contents (GGUF) */
+#define CW_ERR_IO (-6)      /* a file could not be opened, read or mapped */
 
 /* element types of a KV cache */
 #define CW_F32 0
@@ -36,6 +38,7 @@ extern "C" {
 
 typedef struct cw_ctx cw_ctx;
 typedef struct cw_model cw_model;
+typedef struct cw_gguf cw_gguf;
 
 /* ---------------------------------------------------------------- */
 /* Context: device, stream, arena (src/context.rs)                   */
@@ -248,6 +251,82 @@ int cw_model_prefill(cw_model *m, const uint32_t *tokens, int n, int start_pos,
 int cw_model_reset_state(cw_model *m, uint32_t token, int pos);
 /* Download the tokens produced so far by the device-resident loop. */
 int cw_model_tokens(cw_model *m, uint32_t *host_out, int max_n, int *n_out);
+
+/* ---------------------------------------------------------------- */
+/* GGUF container (src/loader/gguf.rs, src/loader/dequant.rs)         */
+/* ---------------------------------------------------------------- */
+
+/* ggml tensor dtypes tensor_f32 decodes (gguf.rs:109-122). */
+#define CW_GGML_F32 0
+#define CW_GGML_F16 1
+#define CW_GGML_Q4_0 2
+#define CW_GGML_Q4_1 3
+#define CW_GGML_Q8_0 8
+#define CW_GGML_Q6_K 14
+
+/* GgufWeights::parse (gguf.rs:68-106) of a file, memory-mapped read-only (the
+ * file is not copied; tensors are decoded from the mapping on request).
+ * Magic "GGUF", version, tensor and metadata counts, the metadata key/values
+ * (kinds 0-12, arrays skipped), the tensor table, then the data section at
+ * the next multiple of general.alignment (default 32).  A repeated key or
+ * tensor name keeps its last entry.  Errors: CW_ERR_IO (open/map),
+ * CW_ERR_FORMAT ("not a GGUF file", truncated header, unknown metadata kind,
+ * data section past the end). */
+int cw_gguf_open(const char *path, cw_gguf **out);
+/* The same over bytes in memory (GgufWeights::parse(bytes)); the bytes are
+ * copied, the caller keeps its buffer. */
+int cw_gguf_parse(const void *bytes, size_t len, cw_gguf **out);
+int cw_gguf_close(cw_gguf *g);
+/* Header facts: version, tensor and metadata counts (distinct names), and the
+ * byte offset of the data section.  Any pointer may be NULL. */
+int cw_gguf_info(const cw_gguf *g, uint32_t *version, uint64_t *n_tensors, uint64_t *n_meta,
+                 uint64_t *data_offset);
+/* Weights::meta_u32 (gguf.rs:165-179): integers truncated to 32 bits, floats
+ * converted like Rust's `as u32` (saturating, NaN -> 0), a missing key 0
+ * except "*vocab_size", which falls back to token_embd.weight's largest dim. */
+int cw_gguf_meta_u32(const cw_gguf *g, const char *key, uint32_t *out);
+/* Weights::meta_f32 (gguf.rs:180-186): floats and integers as f32, missing 0. */
+int cw_gguf_meta_f32(const cw_gguf *g, const char *key, float *out);
+/* A string metadata value (the reference keeps them as Meta::Str without an
+ * accessor): copied NUL-terminated into buf (truncated to buf_len-1 bytes),
+ * its full length in *len_out.  CW_ERR_FORMAT when absent or not a string. */
+int cw_gguf_meta_str(const cw_gguf *g, const char *key, char *buf, size_t buf_len,
+                     size_t *len_out);
+/* Weights::has (gguf.rs:187-189): 1 when the tensor exists, else 0. */
+int cw_gguf_has(const cw_gguf *g, const char *name);
+/* Name of tensor `index` in file order (0 <= index < n_tensors). */
+int cw_gguf_tensor_name(const cw_gguf *g, uint64_t index, char *buf, size_t buf_len);
+/* The tensor table entry: dtype, dims (ne[0] fastest; up to max_dims written),
+ * element count, byte offset inside the data section.  Pointers may be NULL. */
+int cw_gguf_tensor_info(const cw_gguf *g, const char *name, uint32_t *dtype, int *n_dims,
+                        uint64_t *dims, int max_dims, uint64_t *n_elems, uint64_t *offset);
+/* tensor_f32 / matrix_raw / vector_data (gguf.rs:109-122, 201-208): decode a
+ * tensor to f32 in its stored order ([out][in] for a matrix, no transpose),
+ * bit-identical to dequant.rs for F32, F16, Q4_0, Q4_1, Q8_0 and Q6_K.  n must
+ * equal the element count.  Unknown dtype: "tensor NAME: ggml dtype D not
+ * supported yet"; absent: "missing tensor NAME" (both CW_ERR_FORMAT). */
+int cw_gguf_tensor_f32(const cw_gguf *g, const char *name, float *out, size_t n);
+/* A projection [out_f][in_f] (ne0 = in_f) as the split Q4_0 image the GEMV
+ * reads: scales f16 [out_f][in_f/32], quants [out_f][in_f/32][16].  A Q4_0
+ * tensor is repacked block for block (its bytes unchanged); any other dtype is
+ * decoded (cw_gguf_tensor_f32) and quantized by cw_q4_quantize, the
+ * Proj::load + Q4Linear::from_f32 route (layers.rs:103-116). */
+int cw_gguf_tensor_q4(const cw_gguf *g, const char *name, size_t out_f, size_t in_f,
+                      uint16_t *scales, uint8_t *quants);
+/* The model config from the metadata Qwen3::load reads (qwen3.rs:44-53):
+ * qwen3.block_count, .embedding_length, .attention.head_count(_kv),
+ * .attention.key_length, .feed_forward_length, .vocab_size (with the
+ * meta_u32 fallback), .attention.layer_norm_rms_epsilon, .rope.freq_base;
+ * the qwen3 family switches; max_seq and kv_dtype from the caller.  A zero
+ * size, or general.architecture naming another family, is CW_ERR_FORMAT. */
+int cw_gguf_model_config(const cw_gguf *g, int max_seq, int kv_dtype, cw_model_config *cfg);
+/* Qwen3::load's tensor walk (qwen3.rs:56-100) from a GGUF: every layer's
+ * projections through cw_gguf_tensor_q4 and norm gains through
+ * cw_gguf_tensor_f32, output_norm.weight, token_embd.weight decoded to f32,
+ * and output.weight when the file has it (otherwise cw_model_finalize ties
+ * the head to the embedding).  Element counts must match the model's config.
+ * Call cw_model_finalize afterwards. */
+int cw_model_load_gguf(cw_model *m, const cw_gguf *g);
 
 /* ---------------------------------------------------------------- */
 /* Profiling (src/profile.rs, GpuContext::begin_profile/report_profile) */

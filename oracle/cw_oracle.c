@@ -16,6 +16,11 @@
  *   or_f16_to_f32          exhaustive vs numpy float16 + dequant.rs:137-142 KAT
  *   or_f32_to_f16          exhaustive round trip + numpy astype(float16)
  *   or_dequant_q4_0        dequant.rs:190-200 KAT + brute force over d x nibble
+ *   or_dequant_f16         exhaustive over all 65,536 patterns (or_f16_to_f32)
+ *   or_dequant_q8_0        dequant.rs:150-161 KAT; d = 1 -> the int8 bytes
+ *   or_dequant_q4_1        dequant.rs:163-173 KAT; d = 1, m = 0 -> nibble map
+ *   or_dequant_q6_k        dequant.rs:175-188 KAT; round trip through a
+ *                          packer written from ggml's block_q6_K layout
  *   or_quantize_q4_0       q4.rs:37-61: exact-grid round trip, clamp, d==0 case
  *   or_q4_gemv / _refmt    main.rs:120-152 KAT shape, closed forms, f64 truth
  *   or_naive_matmul        closed form (ones -> k), f64 truth
@@ -126,6 +131,69 @@ OR_API void or_dequant_q4_0_soa(const uint16_t *d, const uint8_t *qs, size_t nbl
             uint8_t byte = qs[blk * 16 + j];
             out[blk * 32 + j] = s * (float)((int)(byte & 0x0f) - 8);
             out[blk * 32 + j + 16] = s * (float)((int)(byte >> 4) - 8);
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* The other ggml dtypes tensor_f32 decodes (gguf.rs:109-122)          */
+/* ------------------------------------------------------------------ */
+
+static uint16_t rd_u16(const uint8_t *b, size_t i) { return (uint16_t)(b[i] | (b[i + 1] << 8)); }
+
+/* dequant.rs:37-39: n f16 values. */
+OR_API void or_dequant_f16(const uint8_t *bytes, size_t n, float *out) {
+    for (size_t i = 0; i < n; ++i) out[i] = or_f16_to_f32(rd_u16(bytes, i * 2));
+}
+
+/* dequant.rs:44-56: Q8_0, 34-byte blocks {f16 d, i8 q[32]}, value d*q. */
+OR_API void or_dequant_q8_0(const uint8_t *bytes, size_t n, float *out) {
+    for (size_t blk = 0; blk < n / 32; ++blk) {
+        size_t base = blk * 34;
+        float d = or_f16_to_f32(rd_u16(bytes, base));
+        for (int j = 0; j < 32; ++j) out[blk * 32 + j] = d * (float)(int8_t)bytes[base + 2 + j];
+    }
+}
+
+/* dequant.rs:80-97: Q4_1, 20-byte blocks {f16 d, f16 m, u8 qs[16]};
+ * x[j] = d*(qs[j]&15) + m, x[j+16] = d*(qs[j]>>4) + m. */
+OR_API void or_dequant_q4_1(const uint8_t *bytes, size_t n, float *out) {
+    for (size_t blk = 0; blk < n / 32; ++blk) {
+        size_t base = blk * 20;
+        float d = or_f16_to_f32(rd_u16(bytes, base));
+        float m = or_f16_to_f32(rd_u16(bytes, base + 2));
+        for (int j = 0; j < 16; ++j) {
+            uint8_t byte = bytes[base + 4 + j];
+            out[blk * 32 + j] = d * (float)(byte & 0x0f) + m;
+            out[blk * 32 + j + 16] = d * (float)(byte >> 4) + m;
+        }
+    }
+}
+
+/* dequant.rs:99-131: Q6_K, 210-byte super-blocks of 256 {ql[128], qh[64],
+ * i8 scales[16], f16 d}.  Per half (128 values): for l < 32, four 6-bit
+ * values from ql[l], ql[l+32] (low then high nibbles) and the four 2-bit
+ * fields of qh[l], each scaled by d*scale[is + 2k] with is = l/16. */
+OR_API void or_dequant_q6_k(const uint8_t *bytes, size_t n, float *out) {
+    for (size_t blk = 0; blk < n / 256; ++blk) {
+        const uint8_t *b = bytes + blk * 210;
+        const uint8_t *ql = b, *qh = b + 128;
+        const int8_t *sc = (const int8_t *)(b + 192);
+        float d = or_f16_to_f32(rd_u16(b, 208));
+        float *y = out + blk * 256;
+        for (int half = 0; half < 2; ++half) {
+            int qlo = half * 64, qho = half * 32, sco = half * 8, yo = half * 128;
+            for (int l = 0; l < 32; ++l) {
+                int is = l / 16;
+                int q1 = ((ql[qlo + l] & 0x0f) | (((qh[qho + l] >> 0) & 3) << 4)) - 32;
+                int q2 = ((ql[qlo + l + 32] & 0x0f) | (((qh[qho + l] >> 2) & 3) << 4)) - 32;
+                int q3 = ((ql[qlo + l] >> 4) | (((qh[qho + l] >> 4) & 3) << 4)) - 32;
+                int q4 = ((ql[qlo + l + 32] >> 4) | (((qh[qho + l] >> 6) & 3) << 4)) - 32;
+                y[yo + l] = d * (float)sc[sco + is] * (float)q1;
+                y[yo + l + 32] = d * (float)sc[sco + is + 2] * (float)q2;
+                y[yo + l + 64] = d * (float)sc[sco + is + 4] * (float)q3;
+                y[yo + l + 96] = d * (float)sc[sco + is + 6] * (float)q4;
+            }
         }
     }
 }

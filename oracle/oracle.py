@@ -5,6 +5,7 @@ bench.py's cpu_baseline leg, as the checker.  The product never imports it.
 """
 import ctypes as C
 import os
+import struct
 import subprocess
 
 import numpy as np
@@ -22,6 +23,10 @@ _SIGS = {
     "or_f32_to_f16": (C.c_uint16, [_F]),
     "or_dequant_q4_0": (None, [_P, _SZ, _P]),
     "or_dequant_q4_0_soa": (None, [_P, _P, _SZ, _P]),
+    "or_dequant_f16": (None, [_P, _SZ, _P]),
+    "or_dequant_q8_0": (None, [_P, _SZ, _P]),
+    "or_dequant_q4_1": (None, [_P, _SZ, _P]),
+    "or_dequant_q6_k": (None, [_P, _SZ, _P]),
     "or_quantize_q4_0": (None, [_P, _SZ, _SZ, _P, _P]),
     "or_quantize_q4_0_gguf": (None, [_P, _SZ, _SZ, _P, _P]),
     "or_q4_gemv_refmt": (None, [_P, _P, _P, _I, _I, _P]),
@@ -108,6 +113,149 @@ def dequant_q4_0_soa(scales, quants):
     out = np.empty(s.size * 32, np.float32)
     lib().or_dequant_q4_0_soa(_p(s), _p(q), s.size, _p(out))
     return out
+
+
+def _dequant(fn, raw, n):
+    raw = np.ascontiguousarray(np.frombuffer(bytes(raw), np.uint8))
+    out = np.empty(n, np.float32)
+    getattr(lib(), fn)(_p(raw), n, _p(out))
+    return out
+
+
+def dequant_f16(raw, n):
+    return _dequant("or_dequant_f16", raw, n)
+
+
+def dequant_q8_0(raw, n):
+    return _dequant("or_dequant_q8_0", raw, n)
+
+
+def dequant_q4_1(raw, n):
+    return _dequant("or_dequant_q4_1", raw, n)
+
+
+def dequant_q6_k(raw, n):
+    return _dequant("or_dequant_q6_k", raw, n)
+
+
+# ------------------------------------------------------------------ GGUF container
+
+class OracleGguf:
+    """GgufWeights (src/loader/gguf.rs:30-208) restated in Python over bytes.
+
+    parse follows gguf.rs:68-106 (magic, version u32, n_tensors u64, n_meta
+    u64, metadata, tensor infos, data at the next general.alignment multiple,
+    default 32); metadata values as read_meta_value (gguf.rs:125-151): integer
+    kinds widened (signed ones sign-extended to 64 bits), f32/f64 as float,
+    strings kept, arrays skipped (the element skip of gguf.rs:153-162).  A
+    Python exception (struct.error, IndexError) stands for the reference's
+    panic on a truncated file."""
+
+    _SCALAR = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<B",
+               10: "<Q", 11: "<q", 12: "<d"}
+
+    def __init__(self, data):
+        b = bytes(data)
+        self.p = 0
+        self.b = b
+        if self._take(4) != b"GGUF":
+            raise ValueError("not a GGUF file")
+        self.version = self._u("<I")
+        n_tensors = self._u("<Q")
+        n_meta = self._u("<Q")
+        self.meta = {}
+        for _ in range(n_meta):
+            key = self._str()
+            self.meta[key] = self._value()
+        self.tensors = {}
+        for _ in range(n_tensors):
+            name = self._str()
+            n_dims = self._u("<I")
+            dims = [self._u("<Q") for _ in range(n_dims)]
+            dtype = self._u("<I")
+            offset = self._u("<Q")
+            n = 1
+            for d in dims:
+                n *= d
+            self.tensors[name] = (dtype, dims, n, offset)
+        align = self.meta.get(b"general.alignment", ("other", None))
+        align = align[1] if align[0] == "u" else 32
+        self.data_start = -(-self.p // align) * align
+        if self.data_start > len(b):   # bytes[data_start..] panics in the reference
+            raise IndexError("data section starts past the end")
+        self.data = b[self.data_start:]
+
+    def _take(self, n):
+        if n > len(self.b) - self.p:
+            raise struct.error("truncated")
+        out = self.b[self.p:self.p + n]
+        self.p += n
+        return out
+
+    def _u(self, fmt):
+        return struct.unpack(fmt, self._take(struct.calcsize(fmt)))[0]
+
+    def _str(self):
+        return self._take(self._u("<Q"))
+
+    def _skip(self, t):
+        if t == 8:
+            self._str()
+        elif t in self._SCALAR:
+            self._take(struct.calcsize(self._SCALAR[t]))
+
+    def _value(self):
+        t = self._u("<I")
+        if t in (6, 12):
+            return ("f", float(self._u(self._SCALAR[t])))
+        if t in self._SCALAR:
+            return ("u", self._u(self._SCALAR[t]) & 0xFFFFFFFFFFFFFFFF)
+        if t == 8:
+            return ("s", self._str())
+        if t == 9:
+            et = self._u("<I")
+            for _ in range(self._u("<Q")):
+                self._skip(et)
+        return ("other", None)
+
+    def meta_u32(self, key):
+        """gguf.rs:165-179 (f64 -> u32 saturating like Rust `as`)."""
+        kind, v = self.meta.get(key.encode() if isinstance(key, str) else key, ("other", None))
+        if kind == "u":
+            return v & 0xFFFFFFFF
+        if kind == "f":
+            return 0 if not v > 0 else min(int(v), 0xFFFFFFFF)
+        if key.endswith("vocab_size") and b"token_embd.weight" in self.tensors:
+            return max(self.tensors[b"token_embd.weight"][1] or [0])
+        return 0
+
+    def meta_f32(self, key):
+        """gguf.rs:180-186."""
+        kind, v = self.meta.get(key.encode(), ("other", None))
+        return float(np.float32(v)) if kind in ("u", "f") else 0.0
+
+    def has(self, name):
+        return name.encode() in self.tensors
+
+    def tensor_raw(self, name):
+        dtype, dims, n, off = self.tensors[name.encode()]
+        size = {0: 4 * n, 1: 2 * n, 2: n // 32 * 18, 3: n // 32 * 20, 8: n // 32 * 34,
+                14: n // 256 * 210}[dtype]
+        if off + size > len(self.data):   # the reference's slice panics
+            raise IndexError(f"tensor {name} runs past the data section")
+        return dtype, dims, n, self.data[off:off + size]
+
+    def tensor_f32(self, name):
+        """tensor_f32 (gguf.rs:109-122)."""
+        dtype, dims, n, raw = self.tensor_raw(name)
+        if dtype == 0:
+            return np.frombuffer(raw, np.float32).copy()
+        if dtype == 2:
+            return dequant_q4_0(np.frombuffer(raw, np.uint8), n)
+        fn = {1: dequant_f16, 3: dequant_q4_1, 8: dequant_q8_0, 14: dequant_q6_k}.get(dtype)
+        if fn is None:
+            raise ValueError(f"tensor {name}: ggml dtype {dtype} not supported yet")
+        return fn(raw, n)
 
 
 def quantize_q4_0(data):

@@ -3,7 +3,8 @@
 Run from the repository root: `python tests/golden/make_golden.py`.
 
 reference_kats.json  the literal known answers of the reference's own tests
-                     (src/loader/dequant.rs:133-201, src/main.rs:53-161),
+                     (src/loader/dequant.rs:133-201, src/loader/gguf.rs:219-251,
+                     src/main.rs:53-161),
                      transcribed as data with their citations.
 q4_gemv_kat.npz      the q4_gemv KAT of src/main.rs:120-152 (in=256, out=512,
                      x = fill(0x1234), W = fill(0x5678), quantize_q4_0), with
@@ -34,6 +35,19 @@ KATS = {
     "q4_0_block": {"source": "src/loader/dequant.rs:190-200",
                    "d": 0x3C00, "byte": 8 | (15 << 4),
                    "expect": {"0": 0.0, "16": 7.0}},
+    "q8_0_block": {"source": "src/loader/dequant.rs:150-161",
+                   "d": 0x3800, "quants": "0..31", "expect": {"0": 0.0, "1": 0.5, "10": 5.0}},
+    "q4_1_block": {"source": "src/loader/dequant.rs:163-173",
+                   "d": 0x3C00, "m": 0x3800, "byte": 0 | (15 << 4),
+                   "expect": {"0": 0.5, "16": 15.5}},
+    "q6_k_zero_quants": {"source": "src/loader/dequant.rs:175-188",
+                         "block_bytes": 210, "scales_at": [192, 208], "scale": 1,
+                         "d": 0x3C00, "d_at": 208, "expect": {"0": -32.0, "255": -32.0}},
+    "parse_minimal_gguf": {"source": "src/loader/gguf.rs:219-251",
+                           "version": 3, "meta": {"qwen3.block_count": [4, 28]},
+                           "tensor": {"name": "output_norm.weight", "dims": [4], "dtype": 0,
+                                      "offset": 0, "data": [1.0, 2.0, 3.0, 4.0]},
+                           "alignment": 32},
     "rmsnorm_ones": {"source": "src/main.rs:61-67", "rows": 4, "dim": 1024, "eps": 1e-6},
     "swiglu_const": {"source": "src/main.rs:77-82", "n": 4096, "g": 1.5, "u": -0.7},
     "rope_pos0": {"source": "src/main.rs:93-98", "rows": 16, "head_dim": 128, "theta": 10000.0},
