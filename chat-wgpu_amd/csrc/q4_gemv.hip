@@ -31,9 +31,11 @@
 // beyond the reference's own multiply-add.  8 fma_mix + 5 bit ops per 8
 // weights keeps the VALU below the HBM rate on 256 CUs.
 //
-// Optional prologue: RMSNorm of the raw hidden state (norm.wgsl:20-42) while
-// staging.  Optional epilogues: residual add (ewise.wgsl:9-13) and SwiGLU of
-// a gate/up row pair (glu.wgsl:22-26).
+// Optional prologue: RMSNorm of the raw hidden state (norm.wgsl:20-42) in the
+// same single pass that stages x: x*w is staged and 1/rms(x), a scalar of the
+// row, scales each output sum (the same value up to f32 rounding order).
+// Optional epilogues: residual add (ewise.wgsl:9-13) and SwiGLU of a gate/up
+// row pair (glu.wgsl:22-26).
 
 #include <algorithm>
 #include <map>
@@ -148,6 +150,21 @@ __global__ __launch_bounds__(kThreads, 8) void q4_gemv_kernel(GemvArgs a, int n_
 
     // a ring of PD (tile, block) groups in flight per wave, issued before the
     // activation is staged; slot u always holds group it with it % PD == u
+    // the activation gates the first compute, so its loads go out ahead of
+    // the weights (loads return in issue order); K <= 12288 stays in
+    // registers across the weight issue (K <= 4096 with a norm gain)
+    constexpr int kXR = XS == cwi::XS_RMSNORM ? 1 : 3;
+    const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
+    const float4 *w4 = reinterpret_cast<const float4 *>(a.norm_w);
+    float4 xv[kXR], wn[kXR];
+#pragma unroll
+    for (int j = 0; j < kXR; ++j) {
+        const int idx = tid + j * kThreads;
+        const int ci = idx < K4 ? idx : K4 - 1;
+        xv[j] = x4[ci];
+        if constexpr (XS == cwi::XS_RMSNORM) wn[j] = w4[ci];
+    }
+
     uint4 qv[PD][R];
     uint32_t dv[PD][R];
     int lk = 0, lstep = 0;  // next group to load
@@ -162,40 +179,47 @@ __global__ __launch_bounds__(kThreads, 8) void q4_gemv_kernel(GemvArgs a, int n_
         }
     }
 
-    // ---- stage the activation (optionally RMS-normalised) ----
-    float inv = 1.0f;
-    if constexpr (XS == cwi::XS_RMSNORM) {
-        float ss = 0.0f;
-        for (int i = tid; i < K4; i += kThreads) {
-            float4 v = reinterpret_cast<const float4 *>(a.x)[i];
+    // ---- stage the activation in one pass: x (times the norm gain) into
+    // LDS pre-scaled, with its block sums; the RMS factor 1/rms(x) is a
+    // scalar of the whole row, so it multiplies the row sums in the
+    // epilogue instead of every element here ----
+    float ss = 0.0f;
+    auto stage = [&](int idx, float4 v, float4 w) {
+        if constexpr (XS == cwi::XS_RMSNORM) {
             ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            v.x *= w.x;
+            v.y *= w.y;
+            v.z *= w.z;
+            v.w *= w.w;
         }
+        const int blk = idx >> 3, i = idx & 7;
+        const float sc = i < 4 ? 0x1p24f : 0x1p20f;
+        lds4[i * nb + blk] = make_float4(v.x * sc, v.y * sc, v.z * sc, v.w * sc);
+        // the 8 float4 of a block sit in 8 consecutive lanes (K4 is a
+        // multiple of 8, so they are active together)
+        float part = (v.x + v.y) + (v.z + v.w);
+        part = group_sum<8>(part);
+        if (i == 0) sx[blk] = part;
+    };
+#pragma unroll
+    for (int j = 0; j < kXR; ++j) {
+        const int idx = tid + j * kThreads;
+        if (idx < K4) stage(idx, xv[j], wn[j]);
+    }
+    for (int idx = tid + kXR * kThreads; idx < K4; idx += kThreads)
+        stage(idx, x4[idx], XS == cwi::XS_RMSNORM ? w4[idx] : make_float4(0, 0, 0, 0));
+    if constexpr (XS == cwi::XS_RMSNORM) {
         ss = group_sum<64>(ss);
         if (lane == 0) red[wave] = ss;
-        __syncthreads();
+    }
+    __syncthreads();
+    float inv = 1.0f;
+    if constexpr (XS == cwi::XS_RMSNORM) {
         ss = 0.0f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) ss += red[w];
         inv = 1.0f / sqrtf(ss / (float)K + a.eps);
     }
-    for (int idx = tid; idx < K4; idx += kThreads) {
-        float4 v = reinterpret_cast<const float4 *>(a.x)[idx];
-        if constexpr (XS == cwi::XS_RMSNORM) {
-            float4 w = reinterpret_cast<const float4 *>(a.norm_w)[idx];
-            v.x = (v.x * inv) * w.x;
-            v.y = (v.y * inv) * w.y;
-            v.z = (v.z * inv) * w.z;
-            v.w = (v.w * inv) * w.w;
-        }
-        const int blk = idx >> 3, i = idx & 7;
-        const float sc = i < 4 ? 0x1p24f : 0x1p20f;
-        lds4[i * nb + blk] = make_float4(v.x * sc, v.y * sc, v.z * sc, v.w * sc);
-        // the 8 float4 of a block sit in 8 consecutive lanes
-        float part = (v.x + v.y) + (v.z + v.w);
-        part = group_sum<8>(part);
-        if (i == 0) sx[blk] = part;
-    }
-    __syncthreads();
 
     // ---- stream the weights ----
     float acc[R];
@@ -243,7 +267,10 @@ __global__ __launch_bounds__(kThreads, 8) void q4_gemv_kernel(GemvArgs a, int n_
                 }
                 if (step == S - 1) {  // tile done: reduce over the G lanes of each row, write
 #pragma unroll
-                    for (int r = 0; r < R; ++r) acc[r] = group_sum<G>(acc[r]);
+                    for (int r = 0; r < R; ++r) {
+                        acc[r] = group_sum<G>(acc[r]);
+                        if constexpr (XS == cwi::XS_RMSNORM) acc[r] *= inv;
+                    }
                     if (s == 0) {
                         const int row0 = (wv + k * stride) * T::ROWS;
 #pragma unroll
