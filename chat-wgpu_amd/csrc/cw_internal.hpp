@@ -226,7 +226,8 @@ int launch_argmax(cw_ctx *ctx, const float *logits, int n, uint32_t *out_dev, vo
 // y[M][N] = x[M][K] . W[N][K]^T with x given as bf16 hi/lo rows and W split
 // GGUF Q4_0; EPI_SWIGLU reads a second matrix (B) and stores silu(A x) * (B x).
 struct GemmArgs {
-    const uint16_t *xhi, *xlo;  // [M][K] bf16 bits
+    const uint16_t *xhi, *xlo;  // [M][K] f16 bits, row m scaled by 1 / rowscale[m]
+    const float *rowscale;      // [M] powers of two
     const uint16_t *sA;
     const uint8_t *qA;
     const uint16_t *sB;
@@ -234,12 +235,17 @@ struct GemmArgs {
     const float *resid;  // EPI_ADD: [M][N]
     float *y;            // [M][N]
     int M, N, K;
+    float *part;         // split-K partials (null: no split)
+    size_t part_floats;  // capacity of part
 };
+// K splits the GEMM uses for this shape (the partial workspace holds
+// splits * M * N floats)
+int gemm_splits(const cw_ctx *ctx, Epi epi, int M, int N, int K);
 // token ids on the device (validated < vocab by the caller)
 int launch_embed_rows(cw_ctx *ctx, const float *table, int dim, const uint32_t *tok_dev, int n,
                       float *out);
 int launch_split_rows(cw_ctx *ctx, const float *x, const float *norm_w, float eps, int rows, int K,
-                      uint16_t *hi, uint16_t *lo);
+                      uint16_t *hi, uint16_t *lo, float *rowscale);
 int launch_q4_gemm(cw_ctx *ctx, Epi epi, const GemmArgs &a);
 int launch_qk_rope_kv(cw_ctx *ctx, const float *qkv, const float *qn, const float *kn, float eps,
                       const float *cos_t, const float *sin_t, int M, int n_heads, int n_kv,

@@ -75,6 +75,9 @@ struct cw_model {
     float *pf_hidden = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_attn = nullptr,
           *pf_act = nullptr;
     uint16_t *pf_hi = nullptr, *pf_lo = nullptr;
+    float *pf_rowscale = nullptr;  // per-row powers of two of the GEMM operand split
+    float *pf_part = nullptr;  // split-K partials of the prefill GEMMs
+    size_t pf_part_floats = 0;
     std::vector<void *> pf_allocs;
 
     // fused decode step (one persistent kernel per token)
@@ -399,6 +402,19 @@ int ensure_prefill(cw_model *m, int n) {
     CW_TRY(al((size_t)n * c.hidden * 4, (void **)&m->pf_act));
     CW_TRY(al((size_t)n * wide * 2, (void **)&m->pf_hi));
     CW_TRY(al((size_t)n * wide * 2, (void **)&m->pf_lo));
+    CW_TRY(al((size_t)n * 4, (void **)&m->pf_rowscale));
+    // split-K workspace: the largest splits x M x N of the unfused GEMMs
+    size_t part = 0;
+    const int qkv_n = m->q_dim + 2 * m->kv_dim;
+    const int shapes[3][2] = {{qkv_n, c.dim}, {c.dim, m->q_dim}, {c.dim, c.hidden}};  // N, K
+    for (const auto &sh : shapes) {
+        const int S = gemm_splits(m->ctx, EPI_ADD, n, sh[0], sh[1]);
+        if (S > 1) part = std::max(part, (size_t)S * n * sh[0]);
+    }
+    if (part > 0) {
+        CW_TRY(al(part * 4, (void **)&m->pf_part));
+        m->pf_part_floats = part;
+    }
     m->pf_cap = n;
     return CW_OK;
 }
@@ -407,10 +423,12 @@ int ensure_prefill(cw_model *m, int n) {
 // RMS-normalised) through a Q4_0 matrix pair or single matrix.
 int pf_linear(cw_model *m, const float *x, const float *norm_w, int n, int K, Epi epi,
               const Q4W &w, const Q4W *w2, const float *resid, float *y) {
-    CW_TRY(launch_split_rows(m->ctx, x, norm_w, m->cfg.eps, n, K, m->pf_hi, m->pf_lo));
+    CW_TRY(launch_split_rows(m->ctx, x, norm_w, m->cfg.eps, n, K, m->pf_hi, m->pf_lo,
+                             m->pf_rowscale));
     GemmArgs a{};
     a.xhi = m->pf_hi;
     a.xlo = m->pf_lo;
+    a.rowscale = m->pf_rowscale;
     a.sA = w.s;
     a.qA = w.q;
     if (w2) {
@@ -422,6 +440,8 @@ int pf_linear(cw_model *m, const float *x, const float *norm_w, int n, int K, Ep
     a.M = n;
     a.N = w.out_f;
     a.K = K;
+    a.part = m->pf_part;
+    a.part_floats = m->pf_part_floats;
     return launch_q4_gemm(m->ctx, epi, a);
 }
 

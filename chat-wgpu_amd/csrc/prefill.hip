@@ -8,16 +8,14 @@
 //
 // Precision.  The GEMM and attention must match the f32 per-token path, so no
 // operand is rounded below what the reference computes with:
-//  * Q4_0 weights enter the MFMA as the exact integers q-8 (bf16 holds them
-//    exactly); the block scale d multiplies each 32-wide block's partial sum
-//    in f32 (acc += d * (x . (q-8)), the shader's own order, q4.wgsl:25-82).
-//  * f32 activations are split x = hi + lo with hi = bf16(x) and
-//    lo = bf16(x - hi) (16 significant bits); each block is two MFMAs, hi
-//    and lo, into the same f32 partial.
+//  * GEMM: every Q4_0 weight (q - 8) d enters the f16 MFMAs exactly, as two
+//    f16 parts; each f32 activation row is split into f16 hi + lo (22
+//    significant bits) after an exact power-of-two row scaling (details at
+//    the kernel).  The MFMAs accumulate in f32.
 //  * Attention: K and V are f16 in the cache and enter f16 MFMAs exactly; q
 //    and the softmax weights p are split into f16 hi + lo the same way.
 //
-// MFMA v_mfma_f32_16x16x32_{bf16,f16}: lane l holds A[l % 16][8 (l / 16) + j]
+// MFMA v_mfma_f32_16x16x32_f16: lane l holds A[l % 16][8 (l / 16) + j]
 // and B[8 (l / 16) + j][l % 16] (j = 0..7) and receives D[4 (l / 16) + r][l % 16]
 // (r = 0..3); any k order shared by A and B is valid.
 
@@ -27,9 +25,10 @@
 
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kT = 256;  // threads per workgroup (4 waves)
 
@@ -39,25 +38,22 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// f32 -> bf16 bits, round to nearest even (finite inputs)
-__device__ __forceinline__ uint32_t bf16_bits(float f) {
-    uint32_t u = __builtin_bit_cast(uint32_t, f);
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return u >> 16;
-}
-__device__ __forceinline__ float bf16_val(uint32_t h) { return __builtin_bit_cast(float, h << 16); }
 
 // ---------------------------------------------------------------------------
-// Rows -> bf16 hi/lo (optionally RMS-normalised first, norm.wgsl:20-42).
+// Rows -> f16 hi/lo for the GEMM (optionally RMS-normalised first,
+// norm.wgsl:20-42).  Per row a power of two 2^e brings max|x| into
+// [2^8, 2^9): x 2^-e = hi + lo with hi = f16(.), lo = f16(remainder), and
+// rowscale[row] = 2^e restores the scale in the GEMM epilogue (exactly).
 // One workgroup per row.
 template <bool NORM>
 __global__ __launch_bounds__(kT) void split_rows_kernel(const float *__restrict__ x,
                                                         const float *__restrict__ w, float eps,
                                                         int K, uint16_t *__restrict__ hi,
-                                                        uint16_t *__restrict__ lo) {
+                                                        uint16_t *__restrict__ lo,
+                                                        float *__restrict__ rowscale) {
     __shared__ float red[kT / 64];
     const size_t base = (size_t)blockIdx.x * K;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float inv = 1.0f;
     if constexpr (NORM) {
         float ss = 0.0f;
@@ -66,203 +62,324 @@ __global__ __launch_bounds__(kT) void split_rows_kernel(const float *__restrict_
             ss += v * v;
         }
         ss = wave_sum(ss);
-        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        if (lane == 0) red[wave] = ss;
         __syncthreads();
         ss = (red[0] + red[1]) + (red[2] + red[3]);
         inv = 1.0f / sqrtf(ss / (float)K + eps);
+        __syncthreads();
     }
-    for (int i = tid; i < K; i += kT) {
+    auto value = [&](int i) {
         float v = x[base + i];
         if constexpr (NORM) v = (v * inv) * w[i];
-        const uint32_t h = bf16_bits(v);
-        hi[base + i] = (uint16_t)h;
-        lo[base + i] = (uint16_t)bf16_bits(v - bf16_val(h));
+        return v;
+    };
+    float mx = 0.0f;
+    for (int i = tid; i < K; i += kT) mx = fmaxf(mx, fabsf(value(i)));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const int e = mx > 0.0f ? max(ilogbf(mx) - 8, -100) : 0;
+    const float sc = ldexpf(1.0f, -e);
+    if (tid == 0) rowscale[blockIdx.x] = ldexpf(1.0f, e);
+    for (int i = tid; i < K; i += kT) {
+        const float v = value(i) * sc;  // exact: a power of two
+        const _Float16 h = (_Float16)v;
+        hi[base + i] = __builtin_bit_cast(uint16_t, h);
+        lo[base + i] = __builtin_bit_cast(uint16_t, (_Float16)(v - (float)h));
     }
 }
 
 // ---------------------------------------------------------------------------
 // Q4_0 dequant-GEMM: y[M][N] = x[M][K] . W[N][K]^T (W split GGUF Q4_0).
 //
-// Workgroup tile 128 (rows of x) x 64 (rows of W), four waves of 64 x 32
-// (4 x 2 MFMA tiles of 16 x 16).  Per 32-wide Q4 block the workgroup stages
-// in LDS, double-buffered: the x tile as bf16 hi and lo, and the W tile
-// dequantized once to bf16 (q - 8) with its f32 block scales.  While the
-// waves run the block's MFMAs from one buffer, the next block's global loads
-// are in flight into registers; they are written (and W dequantized) into the
-// other buffer, then one barrier.  LDS rows are padded by 16 B so the 16 lanes
-// of a fragment read hit 16 disjoint bank quads.
-constexpr int kBM = 128, kBN = 64;
-constexpr int kRowB = 64 + 16;  // bytes per LDS row: 32 bf16 + pad
-constexpr int kStageA = kBM * kRowB;          // one of x hi / x lo
-constexpr int kStageB = kBN * kRowB;          // W (q - 8)
-constexpr int kStage = 2 * kStageA + kStageB; // + scales (f32) after
+// Operands, all exact or split exactly into two f16 parts:
+//  * x: per row m a power of two 2^e_m brings max|x| into [2^8, 2^9) (the
+//    split kernel), then x 2^-e_m = x_hi + x_lo with x_hi = f16(.) and x_lo
+//    = f16(remainder): 22 significant bits, no overflow;
+//  * W: the block scale d (f16, 11 bits) = d_hi + d_lo with d_hi rounded to
+//    8 bits and d_lo the 3-bit remainder, and each weight (q - 8) d =
+//    (q - 8) d_hi + (q - 8) d_lo, both parts exact in f16 (at most 11 and 6
+//    significant bits) for |d| < 8192.
+// y = 2^e_m (x_hi W_hi + x_hi W_lo + x_lo W_hi): three f16 MFMAs per
+// 32-wide block accumulate straight into the f32 accumulators, so there is
+// no per-block scaling on the vector ALUs; the dropped x_lo W_lo term is
+// below 2^-19 of each product.
+//
+// Tiling: workgroup tile 128 (rows of x) x 128 (rows of W), four waves in
+// 2 x 2 of 64 x 64 (4 x 4 MFMA tiles of 16 x 16).  K runs one Q4 block per
+// stage, double-buffered in LDS (the x tile hi/lo and the W tile hi/lo, 80 B
+// rows: 64 B + 16 B pad so the 16 lanes of each fragment read hit disjoint
+// bank quads); the next stage's global loads are in flight while the waves
+// run 48 MFMAs from the current buffer.  80 KB of LDS and at most 256
+// registers per lane let two workgroups share a CU, so one workgroup's
+// barrier and load waits overlap the other's MFMAs.
+//
+// SwiGLU: the W tile is 64 gate rows + the same 64 up rows; each wave holds
+// 32 gate and the matching 32 up columns, so silu(g) * u is formed in
+// registers.
+//
+// Work split: tiles are numbered so that the workgroups one XCD receives
+// (consecutive ids go round-robin over the 8 XCDs) share their x rows, which
+// then stay in that XCD's L2 across its N tiles.  When M x N has too few
+// tiles to fill every CU twice, K is split over S workgroups that write f32
+// partials; a second kernel adds them in a fixed order (deterministic) with
+// the epilogue.
+constexpr int kGM = 128, kGN = 128;           // workgroup tile
+constexpr int kGRow = 64 + 16;                // LDS row bytes: 32 f16 + pad
+constexpr int kGA = kGM * kGRow;              // one of x hi / x lo
+constexpr int kGB = kGN * kGRow;              // one of W hi / W lo
+constexpr int kGBuf = 2 * kGA + 2 * kGB;      // 40 KB per stage
+constexpr int kMaxSplit = 8;
 
 __device__ __forceinline__ float f16_bits_val(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
-// 8 nibbles (low or high halves of 8 quant bytes) -> bf16 (q - 8), exact
-__device__ __forceinline__ uint4 dequant8(uint2 q, bool high) {
-    uint32_t w0 = q.x, w1 = q.y;
-    if (high) {
-        w0 >>= 4;
-        w1 >>= 4;
-    }
-    uint32_t p[4];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const uint32_t w = h ? w1 : w0;
-        const float f0 = (float)(int)(w & 15u) - 8.0f;
-        const float f1 = (float)(int)((w >> 8) & 15u) - 8.0f;
-        const float f2 = (float)(int)((w >> 16) & 15u) - 8.0f;
-        const float f3 = (float)(int)((w >> 24) & 15u) - 8.0f;
-        // small integers: the bf16 is the f32's high half, exactly
-        p[2 * h] = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f1),
-                                         __builtin_bit_cast(uint32_t, f0), 0x07060302u);
-        p[2 * h + 1] = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f3),
-                                             __builtin_bit_cast(uint32_t, f2), 0x07060302u);
-    }
-    return make_uint4(p[0], p[1], p[2], p[3]);
+// Nibbles of a quant dword w at bits 4h + {0, 8, 16, 24} (h = 0: the low
+// nibbles, elements 4i..4i+3 of the dword's bytes; h = 1: the high ones)
+// -> the f16 pairs (q - 8) of elements (0, 1) and (2, 3), exactly: 0x6400 | q
+// is the f16 1024 + q.
+__device__ __forceinline__ void nib_pairs(uint32_t w, int h, f16x2 &p01, f16x2 &p23) {
+    const uint32_t s = w >> (4 * h);
+    const uint32_t a = (s & 0x000F000Fu) | 0x64006400u;         // bytes 0, 2
+    const uint32_t b = ((s >> 8) & 0x000F000Fu) | 0x64006400u;  // bytes 1, 3
+    const f16x2 off = {(_Float16)1032.0f, (_Float16)1032.0f};
+    p01 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(b, a, 0x05040100u)) - off;
+    p23 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(b, a, 0x07060302u)) - off;
 }
 
-// Global loads of one block into registers: thread t brings 4 x 16 B of x
-// (hi rows t/2.., lo) and, for t < NM * 64, the 16 quant bytes and the scale
-// of one W row.
-template <int NM>
-struct Stage {
-    uint4 x[4];
-    uint4 q;
-    uint32_t d;
-};
+// One stage in registers: 4 x 16 B of x per thread (128 rows x 64 B, hi
+// then lo) and the 16 quant bytes and the f16 scale of one W row's block
+// (thread pairs share a row: the even thread dequantizes its low nibbles,
+// the odd one its high nibbles).  Native vector registers: an array of
+// HIP's uint4 class is copied with memcpy and stays in scratch memory.
+template <bool SWI>
+__device__ __forceinline__ void w_row(const cwi::GemmArgs &a, int n0, int vc, int *n,
+                                      const uint8_t **q, const uint16_t **s) {
+    if constexpr (SWI) {
+        const bool up = vc >= kGN / 2;
+        *n = n0 + (vc & (kGN / 2 - 1));
+        *q = up ? a.qB : a.qA;
+        *s = up ? a.sB : a.sA;
+    } else {
+        *n = n0 + vc;
+        *q = a.qA;
+        *s = a.sA;
+    }
+}
 
-template <int NM>
-__device__ __forceinline__ void stage_load(const cwi::GemmArgs &a, int nb, int b, int m0, int n0,
-                                           int tid, Stage<NM> &st) {
-    const int bc = b < nb ? b : nb - 1;
-    // x: 128 rows x 64 B (hi) + 128 x 64 B (lo) = 1024 units of 16 B
+// Block kb of the tile; at or past kb_end the scale is 0 (loads clamped in
+// range, so every operand stays finite and the block adds exact zeros).
+template <bool SWI>
+__device__ __forceinline__ void gstage_load(const cwi::GemmArgs &a, int nb, int kb, int kb_end,
+                                            int m0, int n0, int tid, u32x4 (&sx)[4], u32x4 &sq,
+                                            uint32_t &sd) {
+    const int blk = min(kb, nb - 1);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-        const int f = tid + u * kT;             // 0..1023
-        const int half = f >> 9;                // 0: hi, 1: lo
-        const int row = (f >> 2) & (kBM - 1), c = f & 3;
+        const int f = tid + u * kT;              // 0..1023
+        const int half = f >> 9;                 // 0: hi, 1: lo
+        const int row = (f >> 2) & (kGM - 1), c = f & 3;
         const int m = min(m0 + row, a.M - 1);
         const uint16_t *src = half ? a.xlo : a.xhi;
-        st.x[u] = *reinterpret_cast<const uint4 *>(src + (size_t)m * a.K + (size_t)bc * 32 + c * 8);
+        sx[u] = *reinterpret_cast<const u32x4 *>(src + (size_t)m * a.K + (size_t)blk * 32 + c * 8);
     }
-    if (tid < NM * kBN) {
-        const int w = tid >> 6, col = tid & (kBN - 1);
-        const int n = min(n0 + col, a.N - 1);
-        const uint8_t *q = w ? a.qB : a.qA;
-        const uint16_t *s = w ? a.sB : a.sA;
-        const size_t blk = (size_t)n * nb + bc;
-        st.q = *reinterpret_cast<const uint4 *>(q + blk * 16);
-        st.d = s[blk];
-    }
+    int n;
+    const uint8_t *q;
+    const uint16_t *s;
+    w_row<SWI>(a, n0, tid >> 1, &n, &q, &s);
+    const size_t o = (size_t)min(n, a.N - 1) * nb + blk;
+    sq = *reinterpret_cast<const u32x4 *>(q + o * 16);
+    const uint32_t dd = s[o];  // loaded unconditionally, then selected
+    sd = kb < kb_end ? dd : 0u;
 }
 
-template <int NM>
-__device__ __forceinline__ void stage_store(const Stage<NM> &st, unsigned char *buf, int tid) {
+__device__ __forceinline__ void gstage_store(const u32x4 (&sx)[4], u32x4 sq, uint32_t sd,
+                                             unsigned char *buf, int tid) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const int f = tid + u * kT;
         const int half = f >> 9;
-        const int row = (f >> 2) & (kBM - 1), c = f & 3;
-        *reinterpret_cast<uint4 *>(buf + half * kStageA + row * kRowB + c * 16) = st.x[u];
+        const int row = (f >> 2) & (kGM - 1), c = f & 3;
+        *reinterpret_cast<u32x4 *>(buf + half * kGA + row * kGRow + c * 16) = sx[u];
     }
-    if (tid < NM * kBN) {
-        const int w = tid >> 6, col = tid & (kBN - 1);
-        unsigned char *wb = buf + 2 * kStageA + w * (kStageB + kBN * 4);
-        // elements 0..15: low nibbles of bytes 0..15; 16..31: high nibbles
-        const uint2 lo8 = make_uint2(st.q.x, st.q.y), hi8 = make_uint2(st.q.z, st.q.w);
-        *reinterpret_cast<uint4 *>(wb + col * kRowB + 0) = dequant8(lo8, false);
-        *reinterpret_cast<uint4 *>(wb + col * kRowB + 16) = dequant8(hi8, false);
-        *reinterpret_cast<uint4 *>(wb + col * kRowB + 32) = dequant8(lo8, true);
-        *reinterpret_cast<uint4 *>(wb + col * kRowB + 48) = dequant8(hi8, true);
-        reinterpret_cast<float *>(wb + kStageB)[col] = f16_bits_val(st.d);
+    // d = d_hi + d_lo: d_hi the f32 d rounded to 8 significant bits
+    const float d = f16_bits_val(sd);
+    uint32_t u = __builtin_bit_cast(uint32_t, d);
+    u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
+    const float dh = __builtin_bit_cast(float, u);
+    const _Float16 h16 = (_Float16)dh, l16 = (_Float16)(d - dh);  // both exact
+    const f16x2 dh2 = {h16, h16}, dl2 = {l16, l16};
+    // elements 16 h .. 16 h + 15 of the block: nibble half h of bytes 0..15
+    const int vc = tid >> 1, h = tid & 1;
+    u32x4 ph[2], pl[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f16x2 p01, p23;
+        nib_pairs(sq[i], h, p01, p23);
+        const int k = 4 * i;  // elements k..k+3 of this half
+        const f16x2 h01 = p01 * dh2, h23 = p23 * dh2, l01 = p01 * dl2, l23 = p23 * dl2;
+        ph[k >> 3][(k & 7) >> 1] = __builtin_bit_cast(uint32_t, h01);
+        ph[k >> 3][((k & 7) >> 1) + 1] = __builtin_bit_cast(uint32_t, h23);
+        pl[k >> 3][(k & 7) >> 1] = __builtin_bit_cast(uint32_t, l01);
+        pl[k >> 3][((k & 7) >> 1) + 1] = __builtin_bit_cast(uint32_t, l23);
     }
+    unsigned char *wh = buf + 2 * kGA + vc * kGRow + h * 32;
+    unsigned char *wl = wh + kGB;
+    *reinterpret_cast<u32x4 *>(wh) = ph[0];
+    *reinterpret_cast<u32x4 *>(wh + 16) = ph[1];
+    *reinterpret_cast<u32x4 *>(wl) = pl[0];
+    *reinterpret_cast<u32x4 *>(wl + 16) = pl[1];
 }
 
-template <int EPI>
-__global__ __launch_bounds__(kT) void q4_gemm_kernel(cwi::GemmArgs a) {
-    constexpr int NM = EPI == cwi::EPI_SWIGLU ? 2 : 1;  // weight matrices
-    constexpr int kBuf = 2 * kStageA + NM * (kStageB + kBN * 4);
-    __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kBuf];
+// Tile t of MT x NT x S -> (m tile, n tile, split), XCD-grouped when the
+// count divides evenly over the 8 XCDs.
+__device__ __forceinline__ void tile_of(int w, int total, int NT, int MT, int *mt, int *nt,
+                                        int *sp) {
+    int t = w;
+    if ((total & 7) == 0) t = (w & 7) * (total >> 3) + (w >> 3);
+    *nt = t % NT;
+    const int r = t / NT;
+    *mt = r % MT;
+    *sp = r / MT;
+}
+
+// OUT: 0 = the epilogue EPI into y, 1 = f32 partial of split sp into part
+template <int EPI, int OUT>
+__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(2, 2))) void q4_gemm_kernel(
+    cwi::GemmArgs a, int MT, int NT, int S) {
+    constexpr bool SWI = EPI == cwi::EPI_SWIGLU;
+    extern __shared__ __attribute__((aligned(16))) unsigned char glds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 15, lg = lane >> 4;
-    const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
-    const int wr = (wave >> 1) * 64, wc = (wave & 1) * 32;  // wave tile within the block tile
+    int mt, nt, sp;
+    tile_of(blockIdx.x, MT * NT * S, NT, MT, &mt, &nt, &sp);
+    const int m0 = mt * kGM, n0 = nt * (SWI ? kGN / 2 : kGN);
+    const int wm = wave >> 1, wn = wave & 1;
     const int nb = a.K >> 5;
+    // this split's blocks [kb0, kb1), one per stage
+    const int per = (nb + S - 1) / S;
+    const int kb0 = sp * per, kb1 = min(nb, kb0 + per);
+    const int n_st = kb1 - kb0;
 
-    f32x4 acc[NM][4][2];
+    // column tile j of this wave -> virtual column (LDS W row) of its lane
+    int vcol[4];
 #pragma unroll
-    for (int w = 0; w < NM; ++w)
-#pragma unroll
-        for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-            for (int ni = 0; ni < 2; ++ni) acc[w][mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 4; ++j)
+        vcol[j] = SWI ? (j < 2 ? wn * 32 + j * 16 : kGN / 2 + wn * 32 + (j - 2) * 16) + li
+                      : wn * 64 + j * 16 + li;
 
-    Stage<NM> st;
-    stage_load<NM>(a, nb, 0, m0, n0, tid, st);
-    stage_store<NM>(st, lds, tid);
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    u32x4 sx[4], sq;
+    uint32_t sd;
+    if (n_st > 0) {
+        gstage_load<SWI>(a, nb, kb0, kb1, m0, n0, tid, sx, sq, sd);
+        gstage_store(sx, sq, sd, glds, tid);
+    }
     __syncthreads();
-    for (int b = 0; b < nb; ++b) {
-        const unsigned char *cur = lds + (b & 1) * kBuf;
-        stage_load<NM>(a, nb, b + 1, m0, n0, tid, st);  // past the end: a clamped re-load
-        // fragments: A rows wr + 16 mi + li, k 8 lg..; B columns wc + 16 ni + li
-        bf16x8 A[4][2];
+    for (int s = 0; s < n_st; ++s) {
+        const unsigned char *cur = glds + (s & 1) * kGBuf;
+        // next stage's loads, issued before this stage's MFMAs (the last
+        // stage re-loads itself, unused: unconditional loads and stores keep
+        // the loads where they are)
+        gstage_load<SWI>(a, nb, kb0 + min(s + 1, n_st - 1), kb1, m0, n0, tid, sx, sq, sd);
+        __builtin_amdgcn_sched_barrier(0);
+        f16x8 A[4][2], B[4][2];
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi) {
-            const int row = wr + 16 * mi + li;
-            A[mi][0] = *reinterpret_cast<const bf16x8 *>(cur + row * kRowB + lg * 16);
-            A[mi][1] = *reinterpret_cast<const bf16x8 *>(cur + kStageA + row * kRowB + lg * 16);
+        for (int i = 0; i < 4; ++i) {
+            const int row = wm * 64 + 16 * i + li;
+            A[i][0] = *reinterpret_cast<const f16x8 *>(cur + row * kGRow + lg * 16);
+            A[i][1] = *reinterpret_cast<const f16x8 *>(cur + kGA + row * kGRow + lg * 16);
         }
 #pragma unroll
-        for (int w = 0; w < NM; ++w) {
-            const unsigned char *wb = cur + 2 * kStageA + w * (kStageB + kBN * 4);
+        for (int j = 0; j < 4; ++j) {
+            B[j][0] = *reinterpret_cast<const f16x8 *>(cur + 2 * kGA + vcol[j] * kGRow + lg * 16);
+            B[j][1] = *reinterpret_cast<const f16x8 *>(cur + 2 * kGA + kGB + vcol[j] * kGRow +
+                                                       lg * 16);
+        }
 #pragma unroll
-            for (int ni = 0; ni < 2; ++ni) {
-                const int col = wc + 16 * ni + li;
-                const bf16x8 B = *reinterpret_cast<const bf16x8 *>(wb + col * kRowB + lg * 16);
-                const float d = reinterpret_cast<const float *>(wb + kStageB)[col];
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int mi = 0; mi < 4; ++mi) {
-                    f32x4 t = f32x4{0.f, 0.f, 0.f, 0.f};
-                    t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mi][0], B, t, 0, 0, 0);
-                    t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mi][1], B, t, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        acc[w][mi][ni][r] = __builtin_fmaf(d, t[r], acc[w][mi][ni][r]);
-                }
+            for (int j = 0; j < 4; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i][0], B[j][0], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i][0], B[j][1], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i][1], B[j][0], acc[i][j], 0, 0, 0);
             }
-        }
-        stage_store<NM>(st, lds + ((b + 1) & 1) * kBuf, tid);
+        // (after the last stage this fills the idle buffer, which is not read)
+        gstage_store(sx, sq, sd, glds + ((s + 1) & 1) * kGBuf, tid);
         __syncthreads();
     }
 
     // lane holds rows 4 lg + r of each row tile, column li of each column tile
+    constexpr int JN = SWI ? 2 : 4;
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) {
-            const int n = n0 + wc + ni * 16 + li;
+        for (int r = 0; r < 4; ++r) {
+            const int m = m0 + wm * 64 + i * 16 + 4 * lg + r;
+            const float rs = a.rowscale[min(m, a.M - 1)];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = m0 + wr + mi * 16 + 4 * lg + r;
+            for (int j = 0; j < JN; ++j) {
+                const int n = n0 + (SWI ? wn * 32 + j * 16 : wn * 64 + j * 16) + li;
                 if (m < a.M && n < a.N) {
                     const size_t o = (size_t)m * a.N + n;
-                    const float v = acc[0][mi][ni][r];
-                    if constexpr (EPI == cwi::EPI_STORE) {
+                    const float v = acc[i][j][r] * rs;
+                    if constexpr (OUT == 1) {
+                        a.part[(size_t)sp * a.M * a.N + o] = v;
+                    } else if constexpr (EPI == cwi::EPI_STORE) {
                         a.y[o] = v;
                     } else if constexpr (EPI == cwi::EPI_ADD) {
                         a.y[o] = a.resid[o] + v;
                     } else {
-                        const float up = acc[NM - 1][mi][ni][r];
+                        const float up = acc[i][j + 2][r] * rs;
                         a.y[o] = v / (1.0f + expf(-v)) * up;
                     }
                 }
             }
         }
+}
+
+// y = [resid +] sum over s of part[s], s in order (one float4 per thread).
+template <int EPI>
+__global__ __launch_bounds__(kT) void gemm_reduce_kernel(const float *__restrict__ part, int S,
+                                                         size_t n, const float *resid,
+                                                         float *y) {
+    const size_t i = ((size_t)blockIdx.x * kT + threadIdx.x) * 4;
+    if (i >= n) return;
+    const bool vec = ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(resid)) & 15) == 0;
+    if (vec && i + 4 <= n) {
+        float4 v = *reinterpret_cast<const float4 *>(part + i);
+        for (int s = 1; s < S; ++s) {
+            const float4 p = *reinterpret_cast<const float4 *>(part + (size_t)s * n + i);
+            v.x += p.x;
+            v.y += p.y;
+            v.z += p.z;
+            v.w += p.w;
+        }
+        if constexpr (EPI == cwi::EPI_ADD) {
+            const float4 r = *reinterpret_cast<const float4 *>(resid + i);
+            v.x = r.x + v.x;
+            v.y = r.y + v.y;
+            v.z = r.z + v.z;
+            v.w = r.w + v.w;
+        }
+        *reinterpret_cast<float4 *>(y + i) = v;
+        return;
+    }
+    for (size_t e = i; e < n && e < i + 4; ++e) {
+        float v = part[e];
+        for (int s = 1; s < S; ++s) v += part[(size_t)s * n + e];
+        if constexpr (EPI == cwi::EPI_ADD) v = resid[e] + v;
+        y[e] = v;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -515,24 +632,62 @@ int launch_embed_rows(cw_ctx *ctx, const float *table, int dim, const uint32_t *
 }
 
 int launch_split_rows(cw_ctx *ctx, const float *x, const float *norm_w, float eps, int rows, int K,
-                      uint16_t *hi, uint16_t *lo) {
+                      uint16_t *hi, uint16_t *lo, float *rowscale) {
     if (norm_w)
         return launch(ctx, "prefill_split_rmsnorm", split_rows_kernel<true>, dim3(rows), dim3(kT),
-                      0, x, norm_w, eps, K, hi, lo);
+                      0, x, norm_w, eps, K, hi, lo, rowscale);
     return launch(ctx, "prefill_split", split_rows_kernel<false>, dim3(rows), dim3(kT), 0, x,
-                  norm_w, eps, K, hi, lo);
+                  norm_w, eps, K, hi, lo, rowscale);
+}
+
+int gemm_splits(const cw_ctx *ctx, Epi epi, int M, int N, int K) {
+    if (epi == EPI_SWIGLU) return 1;
+    const int tiles = ((M + kGM - 1) / kGM) * ((N + kGN - 1) / kGN);
+    int s = 1;
+    // split K while the workgroups fill less than two per CU and each split
+    // keeps at least 16 blocks
+    while (s < kMaxSplit && s * tiles < 2 * ctx->n_cu && (K / 32) / (2 * s) >= 16) s *= 2;
+    return s;
+}
+
+template <int EPI, int OUT>
+int launch_gemm_tiles(cw_ctx *ctx, const char *label, const GemmArgs &a, int MT, int NT, int S) {
+    auto fn = q4_gemm_kernel<EPI, OUT>;
+    static bool attr = false;  // per instantiation
+    if (!attr) {
+        CW_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(fn),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 2 * kGBuf));
+        attr = true;
+    }
+    return launch(ctx, label, fn, dim3(MT * NT * S), dim3(kT), 2 * kGBuf, a, MT, NT, S);
 }
 
 int launch_q4_gemm(cw_ctx *ctx, Epi epi, const GemmArgs &a) {
-    const dim3 grid((a.N + kBN - 1) / kBN, (a.M + kBM - 1) / kBM);
-    switch (epi) {
-        case EPI_STORE:
-            return launch(ctx, "q4_gemm", q4_gemm_kernel<EPI_STORE>, grid, dim3(kT), 0, a);
-        case EPI_ADD:
-            return launch(ctx, "q4_gemm_add", q4_gemm_kernel<EPI_ADD>, grid, dim3(kT), 0, a);
-        default:
-            return launch(ctx, "q4_gemm_swiglu", q4_gemm_kernel<EPI_SWIGLU>, grid, dim3(kT), 0, a);
+    const int MT = (a.M + kGM - 1) / kGM;
+    if (epi == EPI_SWIGLU)
+        return launch_gemm_tiles<EPI_SWIGLU, 0>(ctx, "q4_gemm_swiglu", a, MT,
+                                                (a.N + kGN / 2 - 1) / (kGN / 2), 1);
+    const int NT = (a.N + kGN - 1) / kGN;
+    const int S = a.part ? gemm_splits(ctx, epi, a.M, a.N, a.K) : 1;
+    if (S > 1 && a.part_floats < (size_t)S * a.M * a.N) {
+        set_error("q4 gemm: split-K workspace of %zu floats, %zu needed", a.part_floats,
+                  (size_t)S * a.M * a.N);
+        return CW_ERR_ARG;
     }
+    if (S == 1)
+        return epi == EPI_ADD ? launch_gemm_tiles<EPI_ADD, 0>(ctx, "q4_gemm_add", a, MT, NT, 1)
+                              : launch_gemm_tiles<EPI_STORE, 0>(ctx, "q4_gemm", a, MT, NT, 1);
+    const int rc = epi == EPI_ADD
+                       ? launch_gemm_tiles<EPI_ADD, 1>(ctx, "q4_gemm_add_splitk", a, MT, NT, S)
+                       : launch_gemm_tiles<EPI_STORE, 1>(ctx, "q4_gemm_splitk", a, MT, NT, S);
+    if (rc != CW_OK) return rc;
+    const size_t n = (size_t)a.M * a.N;
+    const unsigned blocks = (unsigned)((n + 4 * kT - 1) / (4 * kT));
+    if (epi == EPI_ADD)
+        return launch(ctx, "q4_gemm_reduce", gemm_reduce_kernel<EPI_ADD>, dim3(blocks), dim3(kT),
+                      0, (const float *)a.part, S, n, a.resid, a.y);
+    return launch(ctx, "q4_gemm_reduce", gemm_reduce_kernel<EPI_STORE>, dim3(blocks), dim3(kT), 0,
+                  (const float *)a.part, S, n, (const float *)nullptr, a.y);
 }
 
 int launch_qk_rope_kv(cw_ctx *ctx, const float *qkv, const float *qn, const float *kn, float eps,
@@ -567,19 +722,30 @@ extern "C" int cw_q4_gemm(cw_ctx *ctx, const float *x, int m, const uint16_t *sc
     CW_CHECK_ARG(out_f > 0, "cw_q4_gemm: out_f=%d must be positive", out_f);
     CW_CHECK_ARG(((uintptr_t)quants & 15) == 0 && ((uintptr_t)scales & 1) == 0,
                  "cw_q4_gemm: quants must be 16-byte and scales 2-byte aligned");
-    void *scratch = nullptr;
     const size_t n = (size_t)m * in_f;
-    CW_TRY(ctx_scratch(ctx, n * 4, &scratch));
+    const int S = gemm_splits(ctx, EPI_STORE, m, out_f, in_f);
+    const size_t part = S > 1 ? (size_t)S * m * out_f : 0;
+    void *scratch = nullptr;
+    // hi, lo (2 B each per element), row scales, partials (16-byte aligned)
+    const size_t rs_off = (n * 4 + 15) & ~size_t(15);
+    const size_t part_off = (rs_off + (size_t)m * 4 + 15) & ~size_t(15);
+    CW_TRY(ctx_scratch(ctx, part_off + part * 4, &scratch));
     uint16_t *hi = (uint16_t *)scratch, *lo = hi + n;
-    CW_TRY(launch_split_rows(ctx, x, nullptr, 0.0f, m, in_f, hi, lo));
+    float *rs = reinterpret_cast<float *>((char *)scratch + rs_off);
+    CW_TRY(launch_split_rows(ctx, x, nullptr, 0.0f, m, in_f, hi, lo, rs));
     GemmArgs a{};
     a.xhi = hi;
     a.xlo = lo;
+    a.rowscale = rs;
     a.sA = scales;
     a.qA = quants;
     a.y = y;
     a.M = m;
     a.N = out_f;
     a.K = in_f;
+    if (part) {
+        a.part = reinterpret_cast<float *>((char *)scratch + part_off);
+        a.part_floats = part;
+    }
     return launch_q4_gemm(ctx, EPI_STORE, a);
 }

@@ -27,6 +27,7 @@ def rel_err(y, ref):
 GEMM_SHAPES = [  # (m, in_f, out_f)
     (1, 256, 512), (7, 1024, 3072), (64, 4096, 256), (65, 2048, 1024), (37, 96, 100),
     (130, 160, 65), (512, 4096, 512), (200, 12288, 128), (3, 32, 7),
+    (100, 4160, 200),  # K split in two halves of 65 blocks (odd: a half-empty last stage)
 ]
 
 
