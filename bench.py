@@ -103,7 +103,7 @@ def cpu_baseline_8b(cfg, weights, k, v, start_tok, budget_s):
     return n / el, n, el
 
 
-MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 matrix peak
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16 matrix peak
 
 
 def bench_prefill_8b(ctx, m, cfg, P=512, reps=3):
@@ -137,10 +137,11 @@ def bench_prefill_8b(ctx, m, cfg, P=512, reps=3):
         "tok_s": round(P / el, 1), "ms": round(el * 1e3, 3),
         "linear_tflop": round(lin / 1e12, 3), "attention_gflop": round(att / 1e9, 2),
         "gemm_ms": round(gemm_ms, 3),
-        "mfma_util": round(lin / (gemm_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
-        "mfma_util_note": "useful linear flops / GEMM kernel time / 2.5 PFLOP/s dense bf16; "
-                          "each Q4 block issues two MFMAs (activation hi and lo halves, for "
-                          "f32-level parity), so the matrix pipes run twice the useful flops",
+        "mfma_util": round(lin / (gemm_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+        "mfma_util_note": "useful linear flops / GEMM kernel time (incl. split-K reduce) / "
+                          "2.5 PFLOP/s dense fp16; each Q4 block issues three f16 MFMAs "
+                          "(x_hi W_hi, x_hi W_lo, x_lo W_hi: exact split operands for "
+                          "f32-level parity), so the matrix pipes run 3x the useful flops",
         "kernel_ms": {k: round(v, 3) for k, v in prof.items()},
     }
 
@@ -265,6 +266,9 @@ def main():
                     help="for rocprofv3 --pmc runs: one 256 MiB device-to-device copy (the "
                          "counter calibration), then 4 eager decode steps of the workload; "
                          "prints no JSON")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="for rocprofv3 traces of the batched prefill: build the 8B model and "
+                         "print only the 512-token prefill figures (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
@@ -289,6 +293,12 @@ def main():
     m.prefill_kv(k, v, PRE)
     start = int(cw.synth_tokens(cw.synth_key(8008, "start"), 1, cfg.vocab)[0])
     log(f"model ready in {time.perf_counter() - t:.1f}s")
+
+    if args.prefill_only:
+        print(json.dumps(bench_prefill_8b(ctx, m, cfg)), flush=True)
+        m.close()
+        ctx.close()
+        return
 
     if args.probe:
         n = 256 << 20

@@ -132,7 +132,8 @@ int cw_hbm_read_probe(cw_ctx *ctx, const void *buf, size_t bytes, int blocks, ui
 /* Batched form of q4::gemv (src/kernels/q4.rs:9-30): y[m][out_f] = x[m][in_f]
  * . W^T for m rows at once, on the matrix cores (the reference has no batched
  * path; every row equals cw_q4_gemv of that row to within 1e-4 relative).
- * x and y device f32, row-major; quants 16-byte aligned. */
+ * x and y device f32, row-major; quants 16-byte aligned; block scales must be
+ * finite with |d| < 8192 (weights are held as exact f16 parts). */
 int cw_q4_gemm(cw_ctx *ctx, const float *x, int m, const uint16_t *scales, const uint8_t *quants,
                int in_f, int out_f, float *y);
 
@@ -191,7 +192,8 @@ typedef struct cw_model_config {
 int cw_model_create(cw_ctx *ctx, const cw_model_config *cfg, cw_model **out);
 int cw_model_destroy(cw_model *m);
 /* Weights::matrix_raw + Q4Linear (src/model/mod.rs:130-153, layers.rs:74-95),
- * by GGUF name ("blk.3.attn_q.weight", "output.weight", ...). */
+ * by GGUF name ("blk.3.attn_q.weight", "output.weight", ...).  Layer
+ * projections need block scales |d| < 8192 (finite): CW_ERR_ARG otherwise. */
 int cw_model_set_q4(cw_model *m, const char *name, const uint16_t *scales_host,
                     const uint8_t *quants_host);
 /* Weights::vector (norm gains "blk.3.attn_norm.weight", "output_norm.weight";

@@ -70,6 +70,21 @@ def test_q4_gemm_argument_errors(ctx):
         ctx.q4_gemm(x, 0, sd, qd, 64, 64)   # no rows
 
 
+def test_model_rejects_out_of_range_scales(ctx):
+    """A projection block scale |d| >= 8192 (or not finite) is refused at
+    upload: the batched GEMM holds each weight as exact f16 parts."""
+    cfg = cw.make_config(1, 64, 2, 1, 32, 64, 100, 8, cw.CW_F16)
+    m = cw.Model(ctx, cfg)
+    s, q = cw.synth_q4(cw.synth_key(3, "w"), 64, 64, 0.02)
+    for bad in (0x7000, 0xF000, 0x7C00, 0x7E00):   # 8192, -8192, inf, NaN
+        s2 = s.copy()
+        s2[5, 1] = bad
+        with pytest.raises(cw.CwError, match="block 11"):
+            m.set_weights({"blk.0.attn_q.weight": (s2, q)})
+    m.set_weights({"blk.0.attn_q.weight": (s, q)})
+    m.close()
+
+
 def small_f16(max_seq, n_layers=2, dim=256, n_heads=4, n_kv=2, hidden=512, vocab=1000):
     return cw.make_config(n_layers, dim, n_heads, n_kv, 128, hidden, vocab, max_seq, cw.CW_F16,
                           1e-6, 1e6)
