@@ -7,17 +7,21 @@
 //
 // Split over the sequence (flash-decoding).  Workgroup (chunk c, kv head g)
 // owns CP consecutive positions and one wave per query head of the GQA group:
-//   1. the K and V rows of the chunk (this kv head's slice) are loaded with
-//      coalesced 16-byte loads, all issued up front, into an LDS tile with a
-//      16-byte row pad (conflict-free row reads);
-//   2. wave j: lane = position, full q.k dot from the LDS tile against the
-//      query broadcast from LDS (f16 keys feed v_fma_mix directly);
-//      wavefront max / sum give the chunk's softmax partial;
-//   3. wave j: lane = head dimension, P.V over the tile's rows.
+//   1. the query, then the K rows, then the V rows of the chunk (this kv
+//      head's slice) are loaded with coalesced 16-byte loads, all issued up
+//      front in the order they are used, into LDS tiles with a 16-byte row
+//      pad (conflict-free row reads);
+//   2. wave j: lane = position, full q.k dot from the K tile against the
+//      query broadcast from LDS (f16 keys feed v_fma_mix directly) while the
+//      V rows are still arriving; wavefront max / sum give the chunk's
+//      softmax partial;
+//   3. wave j: lane = head dimension, P.V over the V tile's rows.
 // No cross-lane reduction is needed per position.  A chunk partial
 // (max, sum, unnormalised o) goes to HBM unless the sequence fits one chunk,
 // in which case the normalised output is written directly; the merge kernel
-// combines chunks with one round of independent loads.
+// combines chunks with one round of independent loads.  (Scores on the matrix
+// cores were tried for the 4-head groups of the 8B shape: with 4 of 16 MFMA
+// rows used and q / p split into f16 pairs per lane, the kernel ran slower.)
 //
 // Fused prologue (decode step): the raw q/k/v come straight from the fused
 // QKV projection; the kernel applies the per-head QK RMSNorm (norm.wgsl,
@@ -132,7 +136,45 @@ __global__ __launch_bounds__(64 * HPK) void attn_kernel(cwi::AttnArgs a, float s
     const unsigned char *vc = reinterpret_cast<const unsigned char *>(a.v_cache);
     const size_t row_bytes = (size_t)kv_dim * C::ES;
 
-    // ---- 1. issue the K/V tile loads ----
+    // ---- 1. loads, in the order they are needed (they return in issue
+    // order): this wave's query (and, in the workgroup holding the new
+    // position, the new k and v), then the K rows, then the V rows, which
+    // arrive while the scores are computed ----
+    constexpr int QU = (HALF + 63) / 64, VU = (HD + 63) / 64;
+    const int h = g * HPK + wave;
+    float lo[QU], hi[QU], cs[QU], sn[QU], gl[QU], gh[QU];
+    float klo[QU], khi[QU], kgl[QU], kgh[QU], vraw[VU], qp[VU];
+    if (fused) {
+        const float *src = a.qkv + (size_t)h * HD;
+#pragma unroll
+        for (int u = 0; u < QU; ++u) {
+            const int i = min(lane + 64 * u, HALF - 1);
+            lo[u] = src[i];
+            hi[u] = src[i + HALF];
+            cs[u] = a.cos_t[(size_t)pos_new * HALF + i];
+            sn[u] = a.sin_t[(size_t)pos_new * HALF + i];
+            gl[u] = a.q_norm_w[i];
+            gh[u] = a.q_norm_w[i + HALF];
+        }
+        if (has_new && wave == 0) {
+            const int q_dim = a.n_heads * HD;
+            const float *ks = a.qkv + q_dim + g * HD;
+            const float *vs = a.qkv + q_dim + kv_dim + g * HD;
+#pragma unroll
+            for (int u = 0; u < QU; ++u) {
+                const int i = min(lane + 64 * u, HALF - 1);
+                klo[u] = ks[i];
+                khi[u] = ks[i + HALF];
+                kgl[u] = a.k_norm_w[i];
+                kgh[u] = a.k_norm_w[i + HALF];
+            }
+#pragma unroll
+            for (int u = 0; u < VU; ++u) vraw[u] = vs[min(lane + 64 * u, HD - 1)];
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < VU; ++u) qp[u] = a.q[(size_t)h * HD + min(lane + 64 * u, HD - 1)];
+    }
     uint4 kr[C::NLOAD], vr[C::NLOAD];
 #pragma unroll
     for (int i = 0; i < C::NLOAD; ++i) {
@@ -141,86 +183,62 @@ __global__ __launch_bounds__(64 * HPK) void attn_kernel(cwi::AttnArgs a, float s
         int p = c0 + row;
         p = p < seq ? p : seq - 1;
         const size_t off = (size_t)p * row_bytes + (size_t)g * C::ROWB + (size_t)col * 16;
-        if (f < C::CP * C::U4_ROW) {
-            kr[i] = *reinterpret_cast<const uint4 *>(kc + off);
-            vr[i] = *reinterpret_cast<const uint4 *>(vc + off);
-        }
+        if (f < C::CP * C::U4_ROW) kr[i] = *reinterpret_cast<const uint4 *>(kc + off);
+    }
+#pragma unroll
+    for (int i = 0; i < C::NLOAD; ++i) {
+        const int f = tid + i * C::THREADS;
+        const int row = f / C::U4_ROW, col = f % C::U4_ROW;
+        int p = c0 + row;
+        p = p < seq ? p : seq - 1;
+        const size_t off = (size_t)p * row_bytes + (size_t)g * C::ROWB + (size_t)col * 16;
+        if (f < C::CP * C::U4_ROW) vr[i] = *reinterpret_cast<const uint4 *>(vc + off);
     }
 
     // ---- 2. query head of this wave (normalised + rotated when fused) ----
-    float knew[(HALF + 63) / 64][2], vnew[(HD + 63) / 64];
-    {
-        const int h = g * HPK + wave;
-        if (fused) {
-            const float *src = a.qkv + (size_t)h * HD;
-            float lo[(HALF + 63) / 64], hi[(HALF + 63) / 64], cs[(HALF + 63) / 64],
-                sn[(HALF + 63) / 64];
-            float ss = 0.0f;
+    float knew[QU][2], vnew[VU];
+    if (fused) {
+        float ss = 0.0f;
 #pragma unroll
-            for (int u = 0; u < (HALF + 63) / 64; ++u) {
-                const int i = lane + 64 * u;
-                lo[u] = hi[u] = cs[u] = sn[u] = 0.0f;
-                if (i < HALF) {
-                    lo[u] = src[i];
-                    hi[u] = src[i + HALF];
-                    cs[u] = a.cos_t[(size_t)pos_new * HALF + i];
-                    sn[u] = a.sin_t[(size_t)pos_new * HALF + i];
-                    ss += lo[u] * lo[u] + hi[u] * hi[u];
-                }
+        for (int u = 0; u < QU; ++u)
+            if (lane + 64 * u < HALF) ss += lo[u] * lo[u] + hi[u] * hi[u];
+        ss = wave_sum(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)HD + a.eps);
+#pragma unroll
+        for (int u = 0; u < QU; ++u) {
+            const int i = lane + 64 * u;
+            if (i < HALF) {
+                const float l0 = (lo[u] * inv) * gl[u];
+                const float h0 = (hi[u] * inv) * gh[u];
+                q_s[wave * HD + i] = l0 * cs[u] - h0 * sn[u];
+                q_s[wave * HD + i + HALF] = h0 * cs[u] + l0 * sn[u];
             }
-            ss = wave_sum(ss);
-            const float inv = 1.0f / sqrtf(ss / (float)HD + a.eps);
-#pragma unroll
-            for (int u = 0; u < (HALF + 63) / 64; ++u) {
-                const int i = lane + 64 * u;
-                if (i < HALF) {
-                    const float l0 = (lo[u] * inv) * a.q_norm_w[i];
-                    const float h0 = (hi[u] * inv) * a.q_norm_w[i + HALF];
-                    q_s[wave * HD + i] = l0 * cs[u] - h0 * sn[u];
-                    q_s[wave * HD + i + HALF] = h0 * cs[u] + l0 * sn[u];
-                }
-            }
-            if (has_new && wave == 0) {  // the new k (normed + rotated) and v
-                const int q_dim = a.n_heads * HD;
-                const float *ks = a.qkv + q_dim + g * HD;
-                const float *vs = a.qkv + q_dim + kv_dim + g * HD;
-                float kss = 0.0f;
-                float klo[(HALF + 63) / 64], khi[(HALF + 63) / 64];
-#pragma unroll
-                for (int u = 0; u < (HALF + 63) / 64; ++u) {
-                    const int i = lane + 64 * u;
-                    klo[u] = khi[u] = 0.0f;
-                    if (i < HALF) {
-                        klo[u] = ks[i];
-                        khi[u] = ks[i + HALF];
-                        kss += klo[u] * klo[u] + khi[u] * khi[u];
-                    }
-                }
-                kss = wave_sum(kss);
-                const float kinv = 1.0f / sqrtf(kss / (float)HD + a.eps);
-#pragma unroll
-                for (int u = 0; u < (HALF + 63) / 64; ++u) {
-                    const int i = lane + 64 * u;
-                    if (i < HALF) {
-                        const float l0 = (klo[u] * kinv) * a.k_norm_w[i];
-                        const float h0 = (khi[u] * kinv) * a.k_norm_w[i + HALF];
-                        knew[u][0] = l0 * cs[u] - h0 * sn[u];
-                        knew[u][1] = h0 * cs[u] + l0 * sn[u];
-                    }
-                }
-#pragma unroll
-                for (int u = 0; u < (HD + 63) / 64; ++u) {
-                    const int i = lane + 64 * u;
-                    vnew[u] = i < HD ? vs[i] : 0.0f;
-                }
-            }
-        } else {
-            for (int i = lane; i < HD; i += 64) q_s[wave * HD + i] = a.q[(size_t)h * HD + i];
         }
+        if (has_new && wave == 0) {  // the new k (normed + rotated) and v
+            float kss = 0.0f;
+#pragma unroll
+            for (int u = 0; u < QU; ++u)
+                if (lane + 64 * u < HALF) kss += klo[u] * klo[u] + khi[u] * khi[u];
+            kss = wave_sum(kss);
+            const float kinv = 1.0f / sqrtf(kss / (float)HD + a.eps);
+#pragma unroll
+            for (int u = 0; u < QU; ++u) {
+                const float l0 = (klo[u] * kinv) * kgl[u];
+                const float h0 = (khi[u] * kinv) * kgh[u];
+                knew[u][0] = l0 * cs[u] - h0 * sn[u];
+                knew[u][1] = h0 * cs[u] + l0 * sn[u];
+            }
+#pragma unroll
+            for (int u = 0; u < VU; ++u) vnew[u] = vraw[u];
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < VU; ++u)
+            if (lane + 64 * u < HD) q_s[wave * HD + lane + 64 * u] = qp[u];
     }
 
-    // ---- 3. tile -> LDS (rows past the sequence as zeros; the new row from
-    // registers, also to the cache) ----
+    // ---- 3. K tile -> LDS (rows past the sequence as zeros); the new k and
+    // v rows to the cache, the new k row also into the tile ----
 #pragma unroll
     for (int i = 0; i < C::NLOAD; ++i) {
         const int f = tid + i * C::THREADS;
@@ -228,24 +246,21 @@ __global__ __launch_bounds__(64 * HPK) void attn_kernel(cwi::AttnArgs a, float s
             const int row = f / C::U4_ROW, col = f % C::U4_ROW;
             // select per component: a select of whole uint4 lvalues becomes a
             // pointer select that forces kr/vr into scratch memory
-            const bool live = c0 + row < seq;
-            uint4 kk = kr[i], vv = vr[i];
-            if (!live) kk = vv = make_uint4(0, 0, 0, 0);
+            uint4 kk = kr[i];
+            if (c0 + row >= seq) kk = make_uint4(0, 0, 0, 0);
             *reinterpret_cast<uint4 *>(k_t + row * C::ROWP + col * 16) = kk;
-            *reinterpret_cast<uint4 *>(v_t + row * C::ROWP + col * 16) = vv;
         }
     }
     __syncthreads();
     if (has_new && wave == 0) {
         const int r = pos_new - c0;
         KVT *kt = reinterpret_cast<KVT *>(k_t + r * C::ROWP);
-        KVT *vt = reinterpret_cast<KVT *>(v_t + r * C::ROWP);
         KVT *kg = reinterpret_cast<KVT *>(const_cast<unsigned char *>(kc) +
                                           (size_t)pos_new * row_bytes + (size_t)g * C::ROWB);
         KVT *vg = reinterpret_cast<KVT *>(const_cast<unsigned char *>(vc) +
                                           (size_t)pos_new * row_bytes + (size_t)g * C::ROWB);
 #pragma unroll
-        for (int u = 0; u < (HALF + 63) / 64; ++u) {
+        for (int u = 0; u < QU; ++u) {
             const int i = lane + 64 * u;
             if (i < HALF) {
                 const KVT k0 = to_kv<KVT>(knew[u][0]), k1 = to_kv<KVT>(knew[u][1]);
@@ -256,13 +271,9 @@ __global__ __launch_bounds__(64 * HPK) void attn_kernel(cwi::AttnArgs a, float s
             }
         }
 #pragma unroll
-        for (int u = 0; u < (HD + 63) / 64; ++u) {
+        for (int u = 0; u < VU; ++u) {
             const int i = lane + 64 * u;
-            if (i < HD) {
-                const KVT v0 = to_kv<KVT>(vnew[u]);
-                vt[i] = v0;
-                vg[i] = v0;
-            }
+            if (i < HD) vg[i] = to_kv<KVT>(vnew[u]);
         }
     }
     if (has_new) __syncthreads();
@@ -316,7 +327,30 @@ __global__ __launch_bounds__(64 * HPK) void attn_kernel(cwi::AttnArgs a, float s
         if (r < C::CP) p_s[wave * C::CP + r] = pr;
     }
     const float l = wave_sum(lsum);
+
+    // ---- V tile -> LDS (rows past the sequence as zeros), the new v row ----
+#pragma unroll
+    for (int i = 0; i < C::NLOAD; ++i) {
+        const int f = tid + i * C::THREADS;
+        if (f < C::CP * C::U4_ROW) {
+            const int row = f / C::U4_ROW, col = f % C::U4_ROW;
+            uint4 vv = vr[i];
+            if (c0 + row >= seq) vv = make_uint4(0, 0, 0, 0);
+            *reinterpret_cast<uint4 *>(v_t + row * C::ROWP + col * 16) = vv;
+        }
+    }
     __syncthreads();
+    if (has_new) {
+        if (wave == 0) {
+            KVT *vt = reinterpret_cast<KVT *>(v_t + (pos_new - c0) * C::ROWP);
+#pragma unroll
+            for (int u = 0; u < VU; ++u) {
+                const int i = lane + 64 * u;
+                if (i < HD) vt[i] = to_kv<KVT>(vnew[u]);
+            }
+        }
+        __syncthreads();
+    }
 
     // ---- 5. P.V: lane = head dimension, every tile row (masked rows carry
     // p = 0 and a finite clamped V row), unrolled so LDS reads batch up ----
@@ -348,8 +382,7 @@ __global__ __launch_bounds__(64 * HPK) void attn_kernel(cwi::AttnArgs a, float s
         for (int e = 0; e < C::DPL; ++e) o[e] = (o4[e][0] + o4[e][1]) + (o4[e][2] + o4[e][3]);
     }
 
-    // ---- 6. output (one chunk) or chunk partial ----
-    const int h = g * HPK + wave;
+    // ---- 6. output (one chunk) or chunk partial (h: this wave's head) ----
     if (n_chunks == 1) {
         const float inv = 1.0f / l;
         if (d0 < HD)
@@ -386,6 +419,9 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float *
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *po = part + (size_t)h * max_chunks * HD;
     const float *pml = part + (size_t)n_heads * max_chunks * HD + (size_t)h * max_chunks * 2;
+    // this thread's first (max, sum) pair, loaded ahead of the partials (one
+    // round of loads in all; clamped so the load is unconditional)
+    const float2 ml0 = *reinterpret_cast<const float2 *>(pml + 2 * min(tid, nc - 1));
     // first batch of partial elements (thread = element e, chunk slice)
     constexpr int EL = HD < kMergeThreads ? HD : kMergeThreads;
     constexpr int SL = kMergeThreads / EL;  // chunk slices
@@ -397,8 +433,8 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float *
         v[u] = cc < nc ? po[(size_t)cc * HD + e] : 0.0f;
     }
     // (max, sum) over chunks
-    float mx = -INFINITY;
-    for (int cc = tid; cc < nc; cc += kMergeThreads) mx = fmaxf(mx, pml[cc * 2]);
+    float mx = tid < nc ? ml0.x : -INFINITY;
+    for (int cc = tid + kMergeThreads; cc < nc; cc += kMergeThreads) mx = fmaxf(mx, pml[cc * 2]);
     mx = wave_max(mx);
     if (lane == 0) red[wave] = mx;
     __syncthreads();
@@ -407,7 +443,12 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float *
     for (int i = 1; i < kMergeThreads / 64; ++i) M = fmaxf(M, red[i]);
     __syncthreads();
     float ls = 0.0f;
-    for (int cc = tid; cc < nc; cc += kMergeThreads) {
+    if (tid < nc) {
+        const float f = expf(ml0.x - M);
+        w[tid] = f;
+        ls = f * ml0.y;
+    }
+    for (int cc = tid + kMergeThreads; cc < nc; cc += kMergeThreads) {
         const float f = expf(pml[cc * 2] - M);
         w[cc] = f;
         ls += f * pml[cc * 2 + 1];
