@@ -109,12 +109,12 @@ __global__ __launch_bounds__(kT) void split_rows_kernel(const float *__restrict_
 //
 // Tiling: workgroup tile 128 (rows of x) x 128 (rows of W), four waves in
 // 2 x 2 of 64 x 64 (4 x 4 MFMA tiles of 16 x 16).  K runs one Q4 block per
-// stage, double-buffered in LDS (the x tile hi/lo and the W tile hi/lo, 80 B
-// rows: 64 B + 16 B pad so the 16 lanes of each fragment read hit disjoint
-// bank quads); the next stage's global loads are in flight while the waves
-// run 48 MFMAs from the current buffer.  80 KB of LDS and at most 256
-// registers per lane let two workgroups share a CU, so one workgroup's
-// barrier and load waits overlap the other's MFMAs.
+// stage, double-buffered in LDS (the x tile hi/lo and the W tile hi/lo, 64 B
+// rows with XOR-swizzled 16-byte chunks against bank conflicts); the global
+// loads run two stages ahead in registers while the waves run 48 MFMAs per
+// stage from LDS.  64 KB of LDS and at most 256 registers per lane let two
+// workgroups share a CU, so one workgroup's barrier and load waits overlap
+// the other's MFMAs.
 //
 // SwiGLU: the W tile is 64 gate rows + the same 64 up rows; each wave holds
 // 32 gate and the matching 32 up columns, so silu(g) * u is formed in
@@ -127,7 +127,13 @@ __global__ __launch_bounds__(kT) void split_rows_kernel(const float *__restrict_
 // partials; a second kernel adds them in a fixed order (deterministic) with
 // the epilogue.
 constexpr int kGM = 128, kGN = 128;           // workgroup tile
-constexpr int kGRow = 64 + 16;                // LDS row bytes: 32 f16 + pad
+constexpr int kGRow = 64;                     // LDS row bytes: 32 f16
+constexpr int kPre = 2;                       // stages of global loads in flight
+
+// Byte offset of 16-byte chunk c (0..3) in LDS row `row`: the chunk index is
+// XOR-swizzled by (row / 2) % 4, so the 4 lanes per row of a staging store
+// and the 16 rows of a fragment read both spread over distinct bank groups.
+__device__ __forceinline__ int swz(int row, int c) { return (c ^ ((row >> 1) & 3)) << 4; }
 constexpr int kGA = kGM * kGRow;              // one of x hi / x lo
 constexpr int kGB = kGN * kGRow;              // one of W hi / W lo
 constexpr int kGBuf = 2 * kGA + 2 * kGB;      // 40 KB per stage
@@ -203,7 +209,7 @@ __device__ __forceinline__ void gstage_store(const u32x4 (&sx)[4], u32x4 sq, uin
         const int f = tid + u * kT;
         const int half = f >> 9;
         const int row = (f >> 2) & (kGM - 1), c = f & 3;
-        *reinterpret_cast<u32x4 *>(buf + half * kGA + row * kGRow + c * 16) = sx[u];
+        *reinterpret_cast<u32x4 *>(buf + half * kGA + row * kGRow + swz(row, c)) = sx[u];
     }
     // d = d_hi + d_lo: d_hi the f32 d rounded to 8 significant bits
     const float d = f16_bits_val(sd);
@@ -226,12 +232,13 @@ __device__ __forceinline__ void gstage_store(const u32x4 (&sx)[4], u32x4 sq, uin
         pl[k >> 3][(k & 7) >> 1] = __builtin_bit_cast(uint32_t, l01);
         pl[k >> 3][((k & 7) >> 1) + 1] = __builtin_bit_cast(uint32_t, l23);
     }
-    unsigned char *wh = buf + 2 * kGA + vc * kGRow + h * 32;
+    unsigned char *wh = buf + 2 * kGA + vc * kGRow;
     unsigned char *wl = wh + kGB;
-    *reinterpret_cast<u32x4 *>(wh) = ph[0];
-    *reinterpret_cast<u32x4 *>(wh + 16) = ph[1];
-    *reinterpret_cast<u32x4 *>(wl) = pl[0];
-    *reinterpret_cast<u32x4 *>(wl + 16) = pl[1];
+    const int o0 = swz(vc, 2 * h), o1 = swz(vc, 2 * h + 1);
+    *reinterpret_cast<u32x4 *>(wh + o0) = ph[0];
+    *reinterpret_cast<u32x4 *>(wh + o1) = ph[1];
+    *reinterpret_cast<u32x4 *>(wl + o0) = pl[0];
+    *reinterpret_cast<u32x4 *>(wl + o1) = pl[1];
 }
 
 // Tile t of MT x NT x S -> (m tile, n tile, split), XCD-grouped when the
@@ -278,44 +285,57 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    u32x4 sx[4], sq;
-    uint32_t sd;
+    // a ring of kPre register stages: the loads of stage s + 1 + kPre go out
+    // right after stage s + 1 is written to LDS, kPre stages ahead of use;
+    // every load is unconditional (past the end a stage re-loads the last
+    // block, unused), which keeps the registers out of scratch and the loads
+    // where they are issued
+    u32x4 sx[kPre][4], sq[kPre];
+    uint32_t sd[kPre];
     if (n_st > 0) {
-        gstage_load<SWI>(a, nb, kb0, kb1, m0, n0, tid, sx, sq, sd);
-        gstage_store(sx, sq, sd, glds, tid);
+        gstage_load<SWI>(a, nb, kb0, kb1, m0, n0, tid, sx[0], sq[0], sd[0]);
+        gstage_store(sx[0], sq[0], sd[0], glds, tid);
     }
+#pragma unroll
+    for (int u = 0; u < kPre; ++u)
+        gstage_load<SWI>(a, nb, kb0 + min(1 + u, max(n_st - 1, 0)), kb1, m0, n0, tid, sx[u], sq[u],
+                         sd[u]);
     __syncthreads();
-    for (int s = 0; s < n_st; ++s) {
-        const unsigned char *cur = glds + (s & 1) * kGBuf;
-        // next stage's loads, issued before this stage's MFMAs (the last
-        // stage re-loads itself, unused: unconditional loads and stores keep
-        // the loads where they are)
-        gstage_load<SWI>(a, nb, kb0 + min(s + 1, n_st - 1), kb1, m0, n0, tid, sx, sq, sd);
-        __builtin_amdgcn_sched_barrier(0);
-        f16x8 A[4][2], B[4][2];
+    for (int s0 = 0; s0 < n_st; s0 += kPre) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = wm * 64 + 16 * i + li;
-            A[i][0] = *reinterpret_cast<const f16x8 *>(cur + row * kGRow + lg * 16);
-            A[i][1] = *reinterpret_cast<const f16x8 *>(cur + kGA + row * kGRow + lg * 16);
-        }
+        for (int u = 0; u < kPre; ++u) {
+            const int s = s0 + u;
+            if (s < n_st) {
+                const unsigned char *cur = glds + (s & 1) * kGBuf;
+                f16x8 A[4][2], B[4][2];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            B[j][0] = *reinterpret_cast<const f16x8 *>(cur + 2 * kGA + vcol[j] * kGRow + lg * 16);
-            B[j][1] = *reinterpret_cast<const f16x8 *>(cur + 2 * kGA + kGB + vcol[j] * kGRow +
-                                                       lg * 16);
-        }
+                for (int i = 0; i < 4; ++i) {
+                    const int row = wm * 64 + 16 * i + li;
+                    A[i][0] = *reinterpret_cast<const f16x8 *>(cur + row * kGRow + swz(row, lg));
+                    A[i][1] = *reinterpret_cast<const f16x8 *>(cur + kGA + row * kGRow + swz(row, lg));
+                }
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+                for (int j = 0; j < 4; ++j) {
+                    const int o = vcol[j] * kGRow + swz(vcol[j], lg);
+                    B[j][0] = *reinterpret_cast<const f16x8 *>(cur + 2 * kGA + o);
+                    B[j][1] = *reinterpret_cast<const f16x8 *>(cur + 2 * kGA + kGB + o);
+                }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i][0], B[j][0], acc[i][j], 0, 0, 0);
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i][0], B[j][1], acc[i][j], 0, 0, 0);
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i][1], B[j][0], acc[i][j], 0, 0, 0);
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i][0], B[j][0], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i][0], B[j][1], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i][1], B[j][0], acc[i][j], 0, 0, 0);
+                    }
+                // (after the last stage this fills the idle buffer, not read)
+                gstage_store(sx[u], sq[u], sd[u], glds + ((s + 1) & 1) * kGBuf, tid);
+                gstage_load<SWI>(a, nb, kb0 + min(s + 1 + kPre, n_st - 1), kb1, m0, n0, tid, sx[u],
+                                 sq[u], sd[u]);
+                __builtin_amdgcn_sched_barrier(0);
+                __syncthreads();
             }
-        // (after the last stage this fills the idle buffer, which is not read)
-        gstage_store(sx, sq, sd, glds + ((s + 1) & 1) * kGBuf, tid);
-        __syncthreads();
+        }
     }
 
     // lane holds rows 4 lg + r of each row tile, column li of each column tile
