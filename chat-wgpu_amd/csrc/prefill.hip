@@ -51,44 +51,78 @@ __global__ __launch_bounds__(kT) void split_rows_kernel(const float *__restrict_
                                                         int K, uint16_t *__restrict__ hi,
                                                         uint16_t *__restrict__ lo,
                                                         float *__restrict__ rowscale) {
-    __shared__ float red[kT / 64];
+    constexpr int R = 4;  // float4 per thread held in registers (K <= 4096)
+    __shared__ float red[2][kT / 64];
     const size_t base = (size_t)blockIdx.x * K;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    float inv = 1.0f;
-    if constexpr (NORM) {
-        float ss = 0.0f;
-        for (int i = tid; i < K; i += kT) {
-            const float v = x[base + i];
-            ss += v * v;
+    const int K4 = K >> 2;
+    const float4 *x4 = reinterpret_cast<const float4 *>(x + base);
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+    // one pass for the sum of squares and max|x w| (1/rms > 0 is a common
+    // factor, so max|(x/rms) w| = max|x w| / rms)
+    float4 xr[R], wr[R];
+    float ss = 0.0f, mx = 0.0f;
+    auto scan = [&](float4 v, float4 g) {
+        if constexpr (NORM) {
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            v.x *= g.x;
+            v.y *= g.y;
+            v.z *= g.z;
+            v.w *= g.w;
         }
-        ss = wave_sum(ss);
-        if (lane == 0) red[wave] = ss;
-        __syncthreads();
-        ss = (red[0] + red[1]) + (red[2] + red[3]);
-        inv = 1.0f / sqrtf(ss / (float)K + eps);
-        __syncthreads();
-    }
-    auto value = [&](int i) {
-        float v = x[base + i];
-        if constexpr (NORM) v = (v * inv) * w[i];
-        return v;
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     };
-    float mx = 0.0f;
-    for (int i = tid; i < K; i += kT) mx = fmaxf(mx, fabsf(value(i)));
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    if (lane == 0) red[wave] = mx;
+    for (int j = 0; j < R; ++j) {
+        const int i = min(tid + j * kT, K4 - 1);
+        xr[j] = x4[i];
+        if constexpr (NORM) wr[j] = w4[i];
+    }
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+        if (tid + j * kT < K4) scan(xr[j], NORM ? wr[j] : xr[j]);
+    for (int i = tid + R * kT; i < K4; i += kT) scan(x4[i], NORM ? w4[i] : x4[i]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        ss += __shfl_xor(ss, off);
+        mx = fmaxf(mx, __shfl_xor(mx, off));
+    }
+    if (lane == 0) {
+        red[0][wave] = ss;
+        red[1][wave] = mx;
+    }
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    ss = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+    mx = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
+    const float inv = NORM ? 1.0f / sqrtf(ss / (float)K + eps) : 1.0f;
+    mx *= inv;
     const int e = mx > 0.0f ? max(ilogbf(mx) - 8, -100) : 0;
     const float sc = ldexpf(1.0f, -e);
     if (tid == 0) rowscale[blockIdx.x] = ldexpf(1.0f, e);
-    for (int i = tid; i < K; i += kT) {
-        const float v = value(i) * sc;  // exact: a power of two
-        const _Float16 h = (_Float16)v;
-        hi[base + i] = __builtin_bit_cast(uint16_t, h);
-        lo[base + i] = __builtin_bit_cast(uint16_t, (_Float16)(v - (float)h));
-    }
+    auto emit = [&](int i, float4 v, float4 g) {
+        if constexpr (NORM) {
+            v.x = (v.x * inv) * g.x;
+            v.y = (v.y * inv) * g.y;
+            v.z = (v.z * inv) * g.z;
+            v.w = (v.w * inv) * g.w;
+        }
+        const float t[4] = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};  // exact: a power of two
+        uint16_t hb[4], lb[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const _Float16 h = (_Float16)t[k];
+            hb[k] = __builtin_bit_cast(uint16_t, h);
+            lb[k] = __builtin_bit_cast(uint16_t, (_Float16)(t[k] - (float)h));
+        }
+        *reinterpret_cast<uint2 *>(hi + base + 4 * (size_t)i) =
+            make_uint2(hb[0] | (uint32_t)hb[1] << 16, hb[2] | (uint32_t)hb[3] << 16);
+        *reinterpret_cast<uint2 *>(lo + base + 4 * (size_t)i) =
+            make_uint2(lb[0] | (uint32_t)lb[1] << 16, lb[2] | (uint32_t)lb[3] << 16);
+    };
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+        if (tid + j * kT < K4) emit(tid + j * kT, xr[j], NORM ? wr[j] : xr[j]);
+    for (int i = tid + R * kT; i < K4; i += kT) emit(i, x4[i], NORM ? w4[i] : x4[i]);
 }
 
 // ---------------------------------------------------------------------------
