@@ -553,22 +553,36 @@ __global__ __launch_bounds__(kT) void attn_prefill_kernel(const float *__restric
 
     const int last_pos = start + min(q0 + kAttQ, M) - 1;  // last key any row needs
     const int n_tiles = last_pos / kAttK + 1;
-    for (int t = 0; t < n_tiles; ++t) {
-        const int k0 = t * kAttK;
-        __syncthreads();  // previous tile's LDS reads are done
-        // stage K rows and V^T: 64 keys x 128 dims, 16 B per load (4 per thread)
+    // K and V rows of key tile t, 64 keys x 128 dims, 16 B per load (4 each
+    // per thread); the next tile's loads are in flight during this tile's
+    // MFMAs (past the last tile a clamped re-load, unused)
+    u32x4 kn[4], vn[4];
+    auto tile_load = [&](int t) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int f = tid + u * kT;  // 0..1023
             const int key = f >> 4, c8 = (f & 15) * 8;
-            const int p = min(k0 + key, last_pos);
-            const uint4 kv = *reinterpret_cast<const uint4 *>(kc + (size_t)p * kv_dim + g * HD + c8);
-            *reinterpret_cast<uint4 *>(&Ks[key * kKRow + c8]) = kv;
-            const uint4 vv = *reinterpret_cast<const uint4 *>(vc + (size_t)p * kv_dim + g * HD + c8);
-            const _Float16 *ve = reinterpret_cast<const _Float16 *>(&vv);
+            const int p = min(t * kAttK + key, last_pos);
+            kn[u] = *reinterpret_cast<const u32x4 *>(kc + (size_t)p * kv_dim + g * HD + c8);
+            vn[u] = *reinterpret_cast<const u32x4 *>(vc + (size_t)p * kv_dim + g * HD + c8);
+        }
+    };
+    tile_load(0);
+    for (int t = 0; t < n_tiles; ++t) {
+        const int k0 = t * kAttK;
+        __syncthreads();  // previous tile's LDS reads are done
+        // stage K rows and V^T
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int f = tid + u * kT;
+            const int key = f >> 4, c8 = (f & 15) * 8;
+            *reinterpret_cast<u32x4 *>(&Ks[key * kKRow + c8]) = kn[u];
+            const f16x8 ve = __builtin_bit_cast(f16x8, vn[u]);
 #pragma unroll
             for (int j = 0; j < 8; ++j) Vt[(c8 + j) * kVRow + key] = ve[j];
         }
+        tile_load(min(t + 1, n_tiles - 1));
+        __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
 
         // S (16 rows x 64 keys): 4 key tiles of 16, K = 128 dims in 4 steps
