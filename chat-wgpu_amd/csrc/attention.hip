@@ -401,6 +401,14 @@ __global__ __launch_bounds__(64 * HPK) void attn_kernel(cwi::AttnArgs a, float s
     }
 }
 
+// Load of a chunk partial.  Partials are written by other workgroups of the
+// previous kernel, on any XCD, at addresses every call reuses: an agent-scope
+// load misses a line this XCD's L2 may still hold from an earlier call (the
+// release at the end of the writing kernel has put the new data in memory).
+__device__ __forceinline__ float part_load(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Merge of the chunk partials: one workgroup per query head; every partial
 // load is independent and issued before the (max, sum) reduction.
 template <int HD>
@@ -421,7 +429,8 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float *
     const float *pml = part + (size_t)n_heads * max_chunks * HD + (size_t)h * max_chunks * 2;
     // this thread's first (max, sum) pair, loaded ahead of the partials (one
     // round of loads in all; clamped so the load is unconditional)
-    const float2 ml0 = *reinterpret_cast<const float2 *>(pml + 2 * min(tid, nc - 1));
+    const int c0m = min(tid, nc - 1);
+    const float2 ml0 = make_float2(part_load(pml + 2 * c0m), part_load(pml + 2 * c0m + 1));
     // first batch of partial elements (thread = element e, chunk slice)
     constexpr int EL = HD < kMergeThreads ? HD : kMergeThreads;
     constexpr int SL = kMergeThreads / EL;  // chunk slices
@@ -430,11 +439,12 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float *
 #pragma unroll
     for (int u = 0; u < B; ++u) {
         const int cc = sl + SL * u;
-        v[u] = cc < nc ? po[(size_t)cc * HD + e] : 0.0f;
+        v[u] = cc < nc ? part_load(po + (size_t)cc * HD + e) : 0.0f;
     }
     // (max, sum) over chunks
     float mx = tid < nc ? ml0.x : -INFINITY;
-    for (int cc = tid + kMergeThreads; cc < nc; cc += kMergeThreads) mx = fmaxf(mx, pml[cc * 2]);
+    for (int cc = tid + kMergeThreads; cc < nc; cc += kMergeThreads)
+        mx = fmaxf(mx, part_load(pml + cc * 2));
     mx = wave_max(mx);
     if (lane == 0) red[wave] = mx;
     __syncthreads();
@@ -449,9 +459,9 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float *
         ls = f * ml0.y;
     }
     for (int cc = tid + kMergeThreads; cc < nc; cc += kMergeThreads) {
-        const float f = expf(pml[cc * 2] - M);
+        const float f = expf(part_load(pml + cc * 2) - M);
         w[cc] = f;
-        ls += f * pml[cc * 2 + 1];
+        ls += f * part_load(pml + cc * 2 + 1);
     }
     ls = wave_sum(ls);
     if (lane == 0) red[wave] = ls;
@@ -470,7 +480,7 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float *
 #pragma unroll
         for (int u = 0; u < B; ++u) {
             const int cc = cc0 + sl + SL * u;
-            v[u] = cc < nc ? po[(size_t)cc * HD + e] : 0.0f;
+            v[u] = cc < nc ? part_load(po + (size_t)cc * HD + e) : 0.0f;
         }
 #pragma unroll
         for (int u = 0; u < B; ++u) {
