@@ -17,11 +17,20 @@
 //      softmax partial;
 //   3. wave j: lane = head dimension, P.V over the V tile's rows.
 // No cross-lane reduction is needed per position.  A chunk partial
-// (max, sum, unnormalised o) goes to HBM unless the sequence fits one chunk,
-// in which case the normalised output is written directly; the merge kernel
-// combines chunks with one round of independent loads.  (Scores on the matrix
-// cores were tried for the 4-head groups of the 8B shape: with 4 of 16 MFMA
-// rows used and q / p split into f16 pairs per lane, the kernel ran slower.)
+// (max, sum, unnormalised o) goes to memory unless the sequence fits one
+// chunk, in which case the normalised output is written directly.  The last
+// workgroup of a kv head to finish (one agent-scope counter per kv head)
+// merges that head group's partials in the same launch, so the merge costs
+// no kernel boundary.  (Scores on the matrix cores were tried for the 4-head
+// groups of the 8B shape: with 4 of 16 MFMA rows used and q / p split into
+// f16 pairs per lane, the kernel ran slower.)
+//
+// Coherence across the 8 XCDs (one L2 each): partials are written with
+// write-through (sc1) stores and read with sc1 loads, which miss any line an
+// L2 still holds from an earlier call; a workgroup's stores are complete
+// (s_waitcnt) before its counter increment, and the merging workgroup reads
+// only after its own increment returned.  The merger resets the counter, so
+// every launch, eager or replayed from a graph, starts from zero.
 //
 // Fused prologue (decode step): the raw q/k/v come straight from the fused
 // QKV projection; the kernel applies the per-head QK RMSNorm (norm.wgsl,
@@ -38,21 +47,20 @@
 namespace {
 
 constexpr int kMaxChunkSpan = 32768;  // max_seq limit
-// 512 threads: 4 chunk slices x 32 loads per thread cover the 68 chunks of a
-// 4352-position cache in one pass (256 threads took two: 5.6 us against 4.3)
-constexpr int kMergeThreads = 512;
+constexpr int kSc1 = 16;              // buffer-instruction cache policy bits: sc1 (agent scope)
 
 template <typename KVT, int HD, int HPK>
 struct Cfg {
     static constexpr int ES = (int)sizeof(KVT);
     static constexpr int THREADS = 64 * HPK;
-    // 16-byte loads per thread for the K+V tile.  Chunks of <= 64 positions
-    // keep the tile near 36 KB so several workgroups share a CU and every
-    // chunk of a 4K-position cache is resident at once (8 kv heads x 68
-    // chunks = 544 workgroups); small groups load more per thread.
-    static constexpr int LB = THREADS <= 128 ? 32 : 8;
+    // 16-byte loads per thread for the K+V tile.  Chunks of <= 128
+    // positions keep the tile near 70 KB, so two workgroups share a CU and
+    // every chunk of a 4K-position cache is resident at once (8 kv heads x 34
+    // chunks = 272 workgroups), while the merge reads few partials; small
+    // groups load more per thread.
+    static constexpr int LB = THREADS <= 128 ? 32 : 16;
     static constexpr int CP0 = LB * THREADS * 16 / (2 * HD * ES);
-    static constexpr int CP = CP0 > 64 ? 64 : CP0;  // positions per workgroup
+    static constexpr int CP = CP0 > 128 ? 128 : CP0;  // positions per workgroup
     static constexpr int ROWB = HD * ES;              // bytes of one row slice
     static constexpr int ROWP = ROWB + 16;            // padded LDS row stride
     static constexpr int U4_ROW = ROWB / 16;          // 16-byte units per row
@@ -60,8 +68,18 @@ struct Cfg {
     static constexpr int NT = (CP + 63) / 64;         // positions per lane
     static constexpr int DPL = HD >= 64 ? HD / 64 : 1;  // dims per lane in P.V
     static constexpr int EPU = 16 / ES;               // elements per 16 bytes
-    // LDS: K tile, V tile, q [HPK][HD], p [HPK][CP]
-    static constexpr int LDS = 2 * CP * ROWP + HPK * HD * 4 + HPK * CP * 4;
+    // LDS: K tile, V tile, q [HPK][HD], p [HPK][CP]; the merge reuses it
+    // for the chunk weights [HPK][MAXC]
+    static constexpr int MAXC = kMaxChunkSpan / CP;
+    static constexpr int LDS_MAIN = 2 * CP * ROWP + HPK * HD * 4 + HPK * CP * 4;
+    static constexpr int LDS = LDS_MAIN > HPK * MAXC * 4 ? LDS_MAIN : HPK * MAXC * 4;
+    // merge: float4 columns per partial row, chunk slices per wave, partial
+    // rows in flight per lane (one round covers MSL * MB chunks: 36 at
+    // head_dim 128, at most 18 float4 registers)
+    static constexpr int MU = HD / 4;
+    static constexpr int MSL = 64 / MU;
+    static constexpr int MB0 = 36 / MSL > 4 ? 36 / MSL : 4;
+    static constexpr int MB = MB0 < 18 ? MB0 : 18;
     static_assert(LDS <= 160 * 1024, "attention tile exceeds the CU's LDS");
     static_assert(CP >= 8 && CP % 8 == 0, "chunk must hold whole load groups");
 };
@@ -76,6 +94,35 @@ __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
     return v;
+}
+
+// A buffer resource over [p, p + bytes); both wave-uniform (readfirstlane
+// keeps the descriptor in SGPRs).  Loads past `bytes` return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    void *u = reinterpret_cast<void *>(((uint64_t)hi << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(u, 0, __builtin_amdgcn_readfirstlane(bytes),
+                                             0x00020000);
+}
+
+// write-through store of one partial value
+__device__ __forceinline__ void st_part(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// (max, sum) pair of chunk c, read past this XCD's L2 (zeros past the range)
+__device__ __forceinline__ float2 ld_pair(__amdgpu_buffer_rsrc_t r, int c) {
+    return __builtin_bit_cast(float2,
+                              __builtin_amdgcn_raw_buffer_load_b64(r, (uint32_t)c * 8, 0, kSc1));
+}
+
+// every memory operation this wave issued has completed
+__device__ __forceinline__ void drain() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 template <typename T>
@@ -390,119 +437,120 @@ __global__ __launch_bounds__(64 * HPK) void attn_kernel(cwi::AttnArgs a, float s
             for (int e = 0; e < C::DPL; ++e) a.out[(size_t)h * HD + d0 + e] = o[e] * inv;
         return;
     }
-    float *po = a.part + ((size_t)h * max_chunks + c) * HD;
-    if (d0 < HD)
+    float *const part_ml = a.part + (size_t)a.n_heads * max_chunks * HD;
+    {
+        float *po = a.part + ((size_t)h * max_chunks + c) * HD;
+        if (d0 < HD)
 #pragma unroll
-        for (int e = 0; e < C::DPL; ++e) po[d0 + e] = o[e];
-    if (lane == 0) {
-        float *pml = a.part + (size_t)a.n_heads * max_chunks * HD + ((size_t)h * max_chunks + c) * 2;
-        pml[0] = m;
-        pml[1] = l;
+            for (int e = 0; e < C::DPL; ++e) st_part(po + d0 + e, o[e]);
+        if (lane == 0) {
+            float *pml = part_ml + ((size_t)h * max_chunks + c) * 2;
+            st_part(pml, m);
+            st_part(pml + 1, l);
+        }
     }
-}
 
-// Load of a chunk partial.  Partials are written by other workgroups of the
-// previous kernel, on any XCD, at addresses every call reuses: an agent-scope
-// load misses a line this XCD's L2 may still hold from an earlier call (the
-// release at the end of the writing kernel has put the new data in memory).
-__device__ __forceinline__ float part_load(const float *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Merge of the chunk partials: one workgroup per query head; every partial
-// load is independent and issued before the (max, sum) reduction.
-template <int HD>
-__global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float *__restrict__ part,
-                                                                   int n_heads, int cp,
-                                                                   int max_chunks, int seq_host,
-                                                                   const int *__restrict__ pos_dev,
-                                                                   float *__restrict__ out) {
-    constexpr int B = 32;  // chunk loads in flight per thread
-    __shared__ float w[kMaxChunkSpan / 16];
-    __shared__ float red[kMergeThreads / 64];
-    const int h = blockIdx.x;
-    const int seq = pos_dev ? (*pos_dev + 1) : seq_host;
-    const int nc = (seq + cp - 1) / cp;
-    if (nc == 1) return;  // the chunk kernel wrote the output itself
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const float *po = part + (size_t)h * max_chunks * HD;
-    const float *pml = part + (size_t)n_heads * max_chunks * HD + (size_t)h * max_chunks * 2;
-    // this thread's first (max, sum) pair, loaded ahead of the partials (one
-    // round of loads in all; clamped so the load is unconditional)
-    const int c0m = min(tid, nc - 1);
-    const float2 ml0 = make_float2(part_load(pml + 2 * c0m), part_load(pml + 2 * c0m + 1));
-    // first batch of partial elements (thread = element e, chunk slice)
-    constexpr int EL = HD < kMergeThreads ? HD : kMergeThreads;
-    constexpr int SL = kMergeThreads / EL;  // chunk slices
-    const int e = tid % EL, sl = tid / EL;
-    float v[B];
-#pragma unroll
-    for (int u = 0; u < B; ++u) {
-        const int cc = sl + SL * u;
-        v[u] = cc < nc ? part_load(po + (size_t)cc * HD + e) : 0.0f;
+    // ---- 7. arrival: the workgroup's partials are in memory, then one
+    // increment of this kv head's counter; the last arriver merges ----
+    __shared__ int last_s;
+    drain();
+    __syncthreads();
+    if (tid == 0) {
+        unsigned *cnt = a.cnt + 32 * g;
+        const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = old + 1 == (unsigned)n_chunks;
+        if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_s = last;
     }
-    // (max, sum) over chunks
-    float mx = tid < nc ? ml0.x : -INFINITY;
-    for (int cc = tid + kMergeThreads; cc < nc; cc += kMergeThreads)
-        mx = fmaxf(mx, part_load(pml + cc * 2));
-    mx = wave_max(mx);
-    if (lane == 0) red[wave] = mx;
     __syncthreads();
-    float M = red[0];
+    if (!last_s) return;
+
+    // ---- 8. merge of head h over the n_chunks partials (wave = head):
+    // lane (slice sl, float4 column e4) takes chunks sl, sl + MSL, ...; the
+    // (max, sum) pairs of chunks lane and lane + 64 and the first MB partial
+    // rows are all requested before anything waits ----
+    constexpr int MU = C::MU, MSL = C::MSL, MB = C::MB;
+    const int e4 = lane % MU, sl = lane / MU;
+    const __amdgpu_buffer_rsrc_t rp =
+        make_rsrc(a.part + (size_t)h * max_chunks * HD, (uint32_t)(n_chunks * HD * 4));
+    const __amdgpu_buffer_rsrc_t rm =
+        make_rsrc(part_ml + (size_t)h * max_chunks * 2, (uint32_t)(n_chunks * 8));
+    // (the loads are read through bit casts to float vectors: element access
+    // on the builtins' integer results does not give the loaded dwords)
+    const float2 ml_a = ld_pair(rm, lane);
+    const float2 ml_b = ld_pair(rm, lane + 64);
+    // whole byte offsets in the vector offset, which the buffer range check
+    // covers: rows past n_chunks read as zeros
+    const uint32_t voff = (uint32_t)((sl * HD + 4 * e4) * 4);
+    float4 v[MB];
 #pragma unroll
-    for (int i = 1; i < kMergeThreads / 64; ++i) M = fmaxf(M, red[i]);
-    __syncthreads();
+    for (int u = 0; u < MB; ++u)
+        v[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rp, voff + MSL * u * HD * 4, 0, kSc1));
+    const float m_a = ml_a.x, l_a = ml_a.y, m_b = ml_b.x, l_b = ml_b.y;
+    float mx = fmaxf(lane < n_chunks ? m_a : -INFINITY, lane + 64 < n_chunks ? m_b : -INFINITY);
+    for (int cc = lane + 128; cc < n_chunks; cc += 64) {
+        mx = fmaxf(mx, ld_pair(rm, cc).x);
+    }
+    const float M = wave_max(mx);
+    float *wl = reinterpret_cast<float *>(lds) + wave * C::MAXC;  // tiles are no longer read
     float ls = 0.0f;
-    if (tid < nc) {
-        const float f = expf(ml0.x - M);
-        w[tid] = f;
-        ls = f * ml0.y;
+    if (lane < n_chunks) {
+        const float f = expf(m_a - M);
+        wl[lane] = f;
+        ls = f * l_a;
     }
-    for (int cc = tid + kMergeThreads; cc < nc; cc += kMergeThreads) {
-        const float f = expf(part_load(pml + cc * 2) - M);
-        w[cc] = f;
-        ls += f * part_load(pml + cc * 2 + 1);
+    if (lane + 64 < n_chunks) {
+        const float f = expf(m_b - M);
+        wl[lane + 64] = f;
+        ls += f * l_b;
     }
-    ls = wave_sum(ls);
-    if (lane == 0) red[wave] = ls;
-    __syncthreads();
-    float L = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kMergeThreads / 64; ++i) L += red[i];
-    const float inv = 1.0f / L;
-    float acc = 0.0f;
-#pragma unroll
-    for (int u = 0; u < B; ++u) {
-        const int cc = sl + SL * u;
-        if (cc < nc) acc += w[cc] * v[u];
+    for (int cc = lane + 128; cc < n_chunks; cc += 64) {
+        const float2 ml = ld_pair(rm, cc);
+        const float f = expf(ml.x - M);
+        wl[cc] = f;
+        ls += f * ml.y;
     }
-    for (int cc0 = SL * B; cc0 < nc; cc0 += SL * B) {  // more than SL*B chunks
+    const float L = wave_sum(ls);
+    __syncthreads();  // the weights are in LDS
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    auto fold = [&](int cc, float4 x) {
+        const float f = cc < n_chunks ? wl[cc] : 0.0f;
+        acc.x = __builtin_fmaf(f, x.x, acc.x);
+        acc.y = __builtin_fmaf(f, x.y, acc.y);
+        acc.z = __builtin_fmaf(f, x.z, acc.z);
+        acc.w = __builtin_fmaf(f, x.w, acc.w);
+    };
 #pragma unroll
-        for (int u = 0; u < B; ++u) {
-            const int cc = cc0 + sl + SL * u;
-            v[u] = cc < nc ? part_load(po + (size_t)cc * HD + e) : 0.0f;
-        }
+    for (int u = 0; u < MB; ++u) fold(sl + MSL * u, v[u]);
+    // chunks beyond the first round (long caches): rounds of 8 rows per lane
+#pragma unroll 1
+    for (int cc0 = MSL * MB; cc0 < n_chunks; cc0 += MSL * 8) {
+        float4 t[8];
 #pragma unroll
-        for (int u = 0; u < B; ++u) {
-            const int cc = cc0 + sl + SL * u;
-            if (cc < nc) acc += w[cc] * v[u];
-        }
+        for (int u = 0; u < 8; ++u)
+            t[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rp, voff + (cc0 + MSL * u) * HD * 4, 0, kSc1));
+#pragma unroll
+        for (int u = 0; u < 8; ++u) fold(cc0 + sl + MSL * u, t[u]);
     }
-    if constexpr (SL > 1) {  // combine the chunk slices through LDS
-        __shared__ float part_s[kMergeThreads];
-        part_s[tid] = acc;
-        __syncthreads();
-        if (sl == 0) {
-            for (int i = 1; i < SL; ++i) acc += part_s[e + i * EL];
-            out[(size_t)h * HD + e] = acc * inv;
-        }
-    } else {
-        out[(size_t)h * HD + e] = acc * inv;
+    // combine the chunk slices (lanes e4 + MU * s) of each column
+#pragma unroll
+    for (int off = MU; off < 64; off <<= 1) {
+        acc.x += __shfl_xor(acc.x, off);
+        acc.y += __shfl_xor(acc.y, off);
+        acc.z += __shfl_xor(acc.z, off);
+        acc.w += __shfl_xor(acc.w, off);
+    }
+    if (sl == 0) {
+        const float inv = 1.0f / L;
+        *reinterpret_cast<float4 *>(a.out + (size_t)h * HD + 4 * e4) =
+            make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
     }
 }
 
 typedef void (*attn_fn)(cwi::AttnArgs, float, int);
-typedef void (*merge_fn)(const float *, int, int, int, int, const int *, float *);
 
 struct AttnPick {
     attn_fn fn;
@@ -538,17 +586,6 @@ AttnPick pick_hd(int hd, int hpk) {
     }
 }
 
-merge_fn pick_merge(int hd) {
-    switch (hd) {
-        case 16: return attn_merge_kernel<16>;
-        case 32: return attn_merge_kernel<32>;
-        case 64: return attn_merge_kernel<64>;
-        case 128: return attn_merge_kernel<128>;
-        case 256: return attn_merge_kernel<256>;
-        default: return nullptr;
-    }
-}
-
 std::mutex g_mu;
 std::map<const void *, bool> g_lds_set;
 
@@ -580,8 +617,7 @@ size_t attn_scratch_floats(int n_heads, int n_kv, int hd, int max_seq) {
 int launch_attention(cw_ctx *ctx, const AttnArgs &a) {
     const int hpk = a.n_heads / a.n_kv;
     const AttnPick pk = pick_attn(a.kv_dtype, a.hd, hpk);
-    merge_fn mf = pick_merge(a.hd);
-    if (!pk.fn || !mf) {
+    if (!pk.fn) {
         set_error("attention: unsupported head_dim=%d / heads per kv=%d", a.hd, hpk);
         return CW_ERR_ARG;
     }
@@ -589,25 +625,20 @@ int launch_attention(cw_ctx *ctx, const AttnArgs &a) {
         set_error("attention: max_seq=%d exceeds %d", a.max_seq, kMaxChunkSpan);
         return CW_ERR_ARG;
     }
-    CW_TRY(ensure_lds(pk.fn, pk.lds));
-    const int max_chunks = (a.max_seq + pk.cp - 1) / pk.cp;
-    if (max_chunks > kMaxChunkSpan / 16) {  // the merge kernel's weight table
-        set_error("attention: %d chunks of %d positions exceed %d", max_chunks, pk.cp,
-                  kMaxChunkSpan / 16);
+    if (a.n_kv > kMaxAttnKv) {
+        set_error("attention: n_kv_heads=%d exceeds %d", a.n_kv, kMaxAttnKv);
         return CW_ERR_ARG;
     }
+    CW_TRY(ensure_lds(pk.fn, pk.lds));
+    const int max_chunks = (a.max_seq + pk.cp - 1) / pk.cp;
+    AttnArgs b = a;
+    b.cnt = ctx->attn_cnt;
     const float scale = powf((float)a.hd, -0.5f);
     prof_begin(ctx, "attention");
-    hipLaunchKernelGGL(pk.fn, dim3(max_chunks, a.n_kv), dim3(pk.threads), pk.lds, ctx->stream, a,
+    hipLaunchKernelGGL(pk.fn, dim3(max_chunks, a.n_kv), dim3(pk.threads), pk.lds, ctx->stream, b,
                        scale, max_chunks);
     prof_end(ctx);
-    CW_TRY(launch_check("attention"));
-    if (max_chunks == 1) return CW_OK;
-    prof_begin(ctx, "attention_merge");
-    hipLaunchKernelGGL(mf, dim3(a.n_heads), dim3(kMergeThreads), 0, ctx->stream, a.part, a.n_heads,
-                       pk.cp, max_chunks, a.seq, a.pos_dev, a.out);
-    prof_end(ctx);
-    return launch_check("attention_merge");
+    return launch_check("attention");
 }
 
 }  // namespace cwi

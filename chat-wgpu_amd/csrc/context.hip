@@ -207,6 +207,16 @@ int cw_ctx_create(int device, cw_ctx **out) {
         delete ctx;
         return hip_fail(e, "hipStreamCreateWithFlags", __FILE__, __LINE__);
     }
+    const size_t cnt_bytes = (size_t)cwi::kMaxAttnKv * 128;
+    e = hipMalloc(&ctx->attn_cnt, cnt_bytes);
+    if (e == hipSuccess) e = hipMemsetAsync(ctx->attn_cnt, 0, cnt_bytes, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        if (ctx->attn_cnt) hipFree(ctx->attn_cnt);
+        hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return hip_fail(e, "attention counters", __FILE__, __LINE__);
+    }
     *out = ctx;
     return CW_OK;
 }
@@ -218,6 +228,7 @@ int cw_ctx_destroy(cw_ctx *ctx) {
     for (void *p : ctx->allocs) hipFree(p);
     for (auto &c : ctx->chunks) hipFree(c.base);
     if (ctx->scratch) hipFree(ctx->scratch);
+    if (ctx->attn_cnt) hipFree(ctx->attn_cnt);
     for (auto &t : ctx->ropes) {
         hipFree(t.cos_t);
         hipFree(t.sin_t);

@@ -95,6 +95,10 @@ struct cw_ctx {
     std::vector<Chunk> chunks;
     size_t chunk_idx = 0, chunk_off = 0;
 
+    // attention arrival counters, one 128-byte line per kv head, zero
+    // between launches (each launch's merging workgroup resets its own)
+    unsigned *attn_cnt = nullptr;
+
     // kernel scratch (attention partials, argmax partials, counters) for the
     // standalone kernel entry points; grows on demand between launches
     void *scratch = nullptr;
@@ -191,7 +195,11 @@ struct AttnArgs {
     int max_seq;            // grid sizing (positions the cache can hold)
     float *out;             // [n_heads*hd]
     float *part;            // chunk partials, attn_scratch_floats() floats
+    unsigned *cnt;          // set by launch_attention: the context's per-kv-head counters
 };
+
+// kv heads the attention counters cover (cw_ctx::attn_cnt)
+constexpr int kMaxAttnKv = 1024;
 
 size_t attn_scratch_floats(int n_heads, int n_kv, int hd, int max_seq);
 int launch_attention(cw_ctx *ctx, const AttnArgs &a);
