@@ -310,3 +310,15 @@ def test_profile_report(ctx):
         ctx.q4_gemv(xd, sd, qd, 1024, 1024)
     rows = ctx.profile_report()
     assert rows[0][0] == "q4_gemv" and rows[0][1] == 3 and rows[0][2] > 0
+
+
+def test_attention_rejects_more_kv_heads_than_counters(ctx, rng):
+    """The merge counters cover 1024 kv heads; more is an argument error
+    raised before any launch."""
+    nh = nkv = 1025
+    hd = 16
+    q = ctx.storage(rng.standard_normal(nh * hd).astype(np.float32))
+    k = ctx.storage(rng.standard_normal(2 * nkv * hd).astype(np.float32))
+    v = ctx.storage(rng.standard_normal(2 * nkv * hd).astype(np.float32))
+    with pytest.raises(cw.CwError, match="exceeds 1024"):
+        ctx.attention(q, k, v, cw.CW_F32, nh, nkv, 2, hd)
