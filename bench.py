@@ -211,6 +211,29 @@ def bench_single_gemv(ctx, out_f=3072, in_f=1024, pool_bytes=600 << 20, passes=3
     return ms * 1e3 / cnt, q4_bytes(out_f, in_f) + 4 * in_f + 4 * out_f, n
 
 
+def bench_read_probe(ctx, nbytes=2 << 30, passes=4):
+    """Achievable HBM read bandwidth: the read probe (cw_hbm_read_probe, the
+    examples/q4probe.rs analogue) streams one 2 GiB buffer (8x the 256 MB
+    last-level cache) with 16-byte loads, XOR-folded, at 2 to 16 workgroups
+    per CU; kernel timestamps.  Returns {workgroups per CU: GB/s}."""
+    buf = ctx.empty(nbytes // 4, np.uint32)
+    n_cu = ctx.info()["n_cu"]
+    out = ctx.empty(16 * n_cu, np.uint32)
+    res = {}
+    for per_cu in (2, 4, 8, 16):
+        blocks = per_cu * n_cu
+        ctx.hbm_read_probe(buf, nbytes, blocks, out)  # warm
+        ctx.flush()
+        ctx.profile_begin()
+        for _ in range(passes):
+            ctx.hbm_read_probe(buf, nbytes, blocks, out)
+        _, cnt, ms = ctx.profile_report()[0]
+        res[per_cu] = nbytes / (ms * 1e-3 / cnt) / 1e9
+    ctx.free(buf)
+    ctx.free(out)
+    return res
+
+
 def cpu_single_gemv(out_f=3072, in_f=1024, budget_s=1.0):
     """The reference's CPU GEMV paths restated in the oracle, one thread: the
     sequential Q4 dequant-dot (src/main.rs:133-150) and naive_matmul at m=1
@@ -412,6 +435,14 @@ def main():
             "algorithmic_bytes": gb06, "launches": gl06, "us": round(gms06 * 1e3, 2),
             "GB_s": round(gb06 / (gms06 * 1e-3) / 1e9, 1),
             "frac_of_peak": round(gb06 / (gms06 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        rp = bench_read_probe(ctx)
+        best = max(rp.values())
+        ex["hbm_read_probe"] = {
+            "workload": "XOR-fold of a 2 GiB device buffer with 16-byte loads (the reference's "
+                        "q4probe read sweep), kernel timestamps; GB/s by workgroups per CU",
+            "GB_s_by_wg_per_cu": {str(k): round(v, 1) for k, v in rp.items()},
+            "best_GB_s": round(best, 1), "best_frac_of_peak": round(best / HBM_PEAK_GBS, 4),
+            "q4_gemv_frac_of_achievable": round(achieved / best, 4)}
         us1, b1, n1 = bench_single_gemv(ctx)
         ex["single_q4_gemv_3072x1024"] = {
             "workload": f"y[3072] = W x[1024], Q4_0, rotating pool of {n1} weight copies "

@@ -322,3 +322,16 @@ def test_attention_rejects_more_kv_heads_than_counters(ctx, rng):
     v = ctx.storage(rng.standard_normal(2 * nkv * hd).astype(np.float32))
     with pytest.raises(cw.CwError, match="exceeds 1024"):
         ctx.attention(q, k, v, cw.CW_F32, nh, nkv, 2, hd)
+
+
+@pytest.mark.parametrize("n_words,blocks", [(4, 1), (1 << 20, 7), ((1 << 20) + 12, 256)])
+def test_hbm_read_probe_folds_every_word(ctx, rng, n_words, blocks):
+    """The read-bandwidth probe (examples/q4probe.rs's role) reads every
+    16-byte word exactly once: the XOR of its per-workgroup words is the XOR
+    of the whole buffer."""
+    data = rng.integers(0, 1 << 32, n_words, dtype=np.uint64).astype(np.uint32)
+    buf = ctx.storage(data)
+    out = ctx.empty(blocks, np.uint32)
+    ctx.hbm_read_probe(buf, data.nbytes, blocks, out)
+    got = np.bitwise_xor.reduce(out.download())
+    assert int(got) == int(np.bitwise_xor.reduce(data))
