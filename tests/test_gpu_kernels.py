@@ -253,8 +253,10 @@ ATTN_CASES = [  # (n_heads, n_kv, hd, seq, f16)
     (16, 8, 128, 1, False), (16, 8, 128, 33, False), (16, 8, 128, 128, False),
     (16, 8, 128, 129, True), (4, 2, 16, 9, False), (8, 8, 64, 300, True),
     (8, 1, 32, 257, False), (16, 2, 256, 200, True), (64, 8, 128, 1000, True),
-    # more than 256 chunks per head: the merge's multi-pass (max, sum) loops
+    # more than 128 chunks per head: the merge's multi-pass (max, sum) loops
     (32, 8, 128, 9000, False),
+    # f16 cache past one merge round (94 chunks of 128 positions)
+    (32, 8, 128, 12000, True),
 ]
 
 
