@@ -257,8 +257,13 @@ __global__ __launch_bounds__(64 * HPK) void attn_kernel(cwi::AttnArgs a, float s
             if (i < HALF) {
                 const float l0 = (lo[u] * inv) * gl[u];
                 const float h0 = (hi[u] * inv) * gh[u];
-                q_s[wave * HD + i] = l0 * cs[u] - h0 * sn[u];
-                q_s[wave * HD + i + HALF] = h0 * cs[u] + l0 * sn[u];
+                const float r0 = l0 * cs[u] - h0 * sn[u], r1 = h0 * cs[u] + l0 * sn[u];
+                q_s[wave * HD + i] = r0;
+                q_s[wave * HD + i + HALF] = r1;
+                if (a.q_tap && c == 0) {  // the "q" tap (qwen3.rs:165)
+                    a.q_tap[(size_t)h * HD + i] = r0;
+                    a.q_tap[(size_t)h * HD + i + HALF] = r1;
+                }
             }
         }
         if (has_new && wave == 0) {  // the new k (normed + rotated) and v

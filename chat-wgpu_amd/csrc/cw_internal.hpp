@@ -196,6 +196,7 @@ struct AttnArgs {
     float *out;             // [n_heads*hd]
     float *part;            // chunk partials, attn_scratch_floats() floats
     unsigned *cnt;          // set by launch_attention: the context's per-kv-head counters
+    float *q_tap;           // fused path, optional: the normalised, rotated q [n_heads*hd]
 };
 
 // kv heads the attention counters cover (cw_ctx::attn_cnt)

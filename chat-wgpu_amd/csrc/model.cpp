@@ -61,6 +61,11 @@ struct cw_model {
     const float *cos_t = nullptr, *sin_t = nullptr;
     float *hidden = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
     float *hidden_out = nullptr;
+    // hook taps of the last decode step (cw_model_set_taps): "q" [L][q_dim],
+    // "post_attn" and "layer_out" [L][dim]; with taps on, the layers' hidden
+    // states are written straight into them
+    bool taps = false;
+    float *tap_q = nullptr, *tap_post = nullptr, *tap_out = nullptr;
     float *part = nullptr;
     void *argmax_scratch = nullptr;
     GenState *state = nullptr;
@@ -151,14 +156,22 @@ void proj_shape(const cw_model *m, int id, int *out_f, int *in_f) {
     }
 }
 
+// The hidden state after the last layer of a decode step.
+float *last_hidden(cw_model *m) {
+    return m->taps ? m->tap_out + (size_t)(m->cfg.n_layers - 1) * m->cfg.dim : m->hidden;
+}
+
 int enqueue_step(cw_model *m) {
     cw_ctx *ctx = m->ctx;
     const auto &c = m->cfg;
     CW_TRY(launch_embed(ctx, m->embed, c.vocab, c.dim, &m->state->token, m->hidden));
+    float *h_in = m->hidden;  // this layer's input; updated in place unless taps are on
     for (int i = 0; i < c.n_layers; ++i) {
         Layer &L = m->layers[i];
+        float *h_post = m->taps ? m->tap_post + (size_t)i * c.dim : h_in;
+        float *h_out = m->taps ? m->tap_out + (size_t)i * c.dim : h_post;
         GemvArgs g{};
-        g.x = m->hidden;
+        g.x = h_in;
         g.norm_w = L.attn_norm;
         g.eps = c.eps;
         g.sA = L.qkv.s;
@@ -185,20 +198,21 @@ int enqueue_step(cw_model *m) {
         a.max_seq = c.max_seq;
         a.out = m->attn;
         a.part = m->part;
+        a.q_tap = m->taps ? m->tap_q + (size_t)i * m->q_dim : nullptr;
         CW_TRY(launch_attention(ctx, a));
 
         g = GemvArgs{};
         g.x = m->attn;
         g.sA = L.wo.s;
         g.qA = L.wo.q;
-        g.resid = m->hidden;
-        g.y = m->hidden;
+        g.resid = h_in;
+        g.y = h_post;
         g.K = m->q_dim;
         g.N = c.dim;
         CW_TRY(launch_q4_gemv(ctx, XS_PLAIN, EPI_ADD, g));
 
         g = GemvArgs{};
-        g.x = m->hidden;
+        g.x = h_post;
         g.norm_w = L.ffn_norm;
         g.eps = c.eps;
         g.sA = L.gate.s;
@@ -214,14 +228,15 @@ int enqueue_step(cw_model *m) {
         g.x = m->act;
         g.sA = L.down.s;
         g.qA = L.down.q;
-        g.resid = m->hidden;
-        g.y = m->hidden;
+        g.resid = h_post;
+        g.y = h_out;
         g.K = c.hidden;
         g.N = c.dim;
         CW_TRY(launch_q4_gemv(ctx, XS_PLAIN, EPI_ADD, g));
+        h_in = h_out;
     }
     GemvArgs g{};
-    g.x = m->hidden;
+    g.x = h_in;
     g.norm_w = m->final_norm;
     g.eps = c.eps;
     g.sA = m->lm_head.s;
@@ -781,7 +796,7 @@ int cw_model_step(cw_model *m, uint32_t token, int pos, uint32_t *argmax_out) {
     GenState s{pos, token, pos, 0, 0, 0};
     CW_TRY(set_state(m, s));
     CW_TRY(enqueue_step(m));
-    CW_TRY(launch_rmsnorm(m->ctx, m->hidden, m->final_norm, 1, m->cfg.dim, m->cfg.eps,
+    CW_TRY(launch_rmsnorm(m->ctx, last_hidden(m), m->final_norm, 1, m->cfg.dim, m->cfg.eps,
                           m->hidden_out));
     uint32_t r = 0;
     CW_HIP(hipMemcpyAsync(&r, m->argmax_out, 4, hipMemcpyDeviceToHost, m->ctx->stream));
@@ -798,6 +813,57 @@ int cw_model_logits(cw_model *m, float *host_out) {
 int cw_model_hidden(cw_model *m, float *host_out) {
     CW_CHECK_ARG(m && host_out, "cw_model_hidden: null argument");
     return cw_download(m->ctx, host_out, m->hidden_out, (size_t)m->cfg.dim * 4);
+}
+
+int cw_model_set_taps(cw_model *m, int enable) {
+    CW_CHECK_ARG(m != nullptr, "cw_model_set_taps: null model");
+    const auto &c = m->cfg;
+    if (enable && !m->tap_q) {
+        CW_TRY(dalloc(m, (size_t)c.n_layers * m->q_dim * 4, (void **)&m->tap_q));
+        CW_TRY(dalloc(m, (size_t)c.n_layers * c.dim * 4, (void **)&m->tap_post));
+        CW_TRY(dalloc(m, (size_t)c.n_layers * c.dim * 4, (void **)&m->tap_out));
+        CW_HIP(hipMemsetAsync(m->tap_q, 0, (size_t)c.n_layers * m->q_dim * 4, m->ctx->stream));
+        CW_HIP(hipMemsetAsync(m->tap_post, 0, (size_t)c.n_layers * c.dim * 4, m->ctx->stream));
+        CW_HIP(hipMemsetAsync(m->tap_out, 0, (size_t)c.n_layers * c.dim * 4, m->ctx->stream));
+    }
+    if ((enable != 0) != m->taps) {
+        // the captured step holds the other buffer addresses: capture again
+        CW_HIP(hipStreamSynchronize(m->ctx->stream));
+        if (m->graph_exec) CW_HIP(hipGraphExecDestroy(m->graph_exec));
+        if (m->graph) CW_HIP(hipGraphDestroy(m->graph));
+        m->graph_exec = nullptr;
+        m->graph = nullptr;
+        m->taps = enable != 0;
+    }
+    return CW_OK;
+}
+
+int cw_model_tap(cw_model *m, const char *name, int layer, float *host_out, int len) {
+    CW_CHECK_ARG(m && name && host_out, "cw_model_tap: null argument");
+    const auto &c = m->cfg;
+    if (!m->taps) {
+        set_error("cw_model_tap: taps are off (cw_model_set_taps)");
+        return CW_ERR_STATE;
+    }
+    CW_CHECK_ARG(layer >= 0 && layer < c.n_layers, "cw_model_tap: layer %d outside [0, %d)",
+                 layer, c.n_layers);
+    const float *src = nullptr;
+    int n = 0;
+    if (!strcmp(name, "q")) {
+        src = m->tap_q + (size_t)layer * m->q_dim;
+        n = m->q_dim;
+    } else if (!strcmp(name, "post_attn")) {
+        src = m->tap_post + (size_t)layer * c.dim;
+        n = c.dim;
+    } else if (!strcmp(name, "layer_out")) {
+        src = m->tap_out + (size_t)layer * c.dim;
+        n = c.dim;
+    } else {
+        set_error("cw_model_tap: unknown tap '%s' (q, post_attn, layer_out)", name);
+        return CW_ERR_ARG;
+    }
+    CW_CHECK_ARG(len == n, "cw_model_tap: tap '%s' holds %d floats, len=%d", name, n, len);
+    return cw_download(m->ctx, host_out, src, (size_t)n * 4);
 }
 
 int cw_generate(cw_model *m, const uint32_t *prompt, int n_prompt, int max_new, int start_pos,
@@ -860,7 +926,8 @@ int cw_model_prefill(cw_model *m, const uint32_t *tokens, int n, int start_pos,
         GenState s{start_pos, tokens[0], start_pos, n, 0, 0};
         CW_TRY(set_state(m, s));
         CW_TRY(run_steps(m, n, CW_STEP_EAGER));
-        CW_TRY(launch_rmsnorm(m->ctx, m->hidden, m->final_norm, 1, c.dim, c.eps, m->hidden_out));
+        CW_TRY(launch_rmsnorm(m->ctx, last_hidden(m), m->final_norm, 1, c.dim, c.eps,
+                              m->hidden_out));
     }
     uint32_t r = 0;
     CW_HIP(hipMemcpyAsync(&r, m->argmax_out, 4, hipMemcpyDeviceToHost, m->ctx->stream));

@@ -92,6 +92,8 @@ _SIGS = {
     "cw_model_step": (_I, [_P, _U32, _I, C.POINTER(_U32)]),
     "cw_model_logits": (_I, [_P, _P]),
     "cw_model_hidden": (_I, [_P, _P]),
+    "cw_model_set_taps": (_I, [_P, _I]),
+    "cw_model_tap": (_I, [_P, C.c_char_p, _I, _P, _I]),
     "cw_generate": (_I, [_P, _P, _I, _I, _I, _I, _P]),
     "cw_model_decode_async": (_I, [_P, _I, _I]),
     "cw_model_reset_state": (_I, [_P, _U32, _I]),
@@ -530,6 +532,21 @@ class Model:
     def hidden(self):
         out = np.empty(self.cfg.dim, np.float32)
         check(lib().cw_model_hidden(self.h, _ptr(out)))
+        return out
+
+    def set_taps(self, enable=True):
+        """Keep the forward's hook taps of every decode step (the reference's
+        Hook / Capture, mod.rs:158-165, main.rs:193-207)."""
+        check(lib().cw_model_set_taps(self.h, 1 if enable else 0))
+
+    TAP_NAMES = ("q", "post_attn", "layer_out")
+
+    def tap(self, name, layer):
+        """The tap `name` ("q", "post_attn" or "layer_out") of `layer` from
+        the last decode step."""
+        n = self.cfg.n_heads * self.cfg.head_dim if name == "q" else self.cfg.dim
+        out = np.empty(n, np.float32)
+        check(lib().cw_model_tap(self.h, name.encode(), int(layer), _ptr(out), n))
         return out
 
     def generate(self, prompt, max_new, start_pos=0, mode=STEP_GRAPH):

@@ -215,6 +215,17 @@ int cw_model_step(cw_model *m, uint32_t token, int pos, uint32_t *argmax_out);
 int cw_model_logits(cw_model *m, float *host_out);
 /* Download the final hidden state [dim] (post final norm) of the last step. */
 int cw_model_hidden(cw_model *m, float *host_out);
+/* Hook (src/model/mod.rs:158-165) in the shape of main.rs's Capture hook
+ * (main.rs:193-207): with taps on, every decode step (eager or graph) keeps
+ * the forward's taps of each layer: "q" after QK-norm and RoPE
+ * (qwen3.rs:165, n_heads*head_dim floats), "post_attn" after the attention
+ * residual (qwen3.rs:180, dim floats) and "layer_out" (qwen3.rs:188, dim
+ * floats).  Toggling re-captures the graph step; the batched prompt phase
+ * records no taps. */
+int cw_model_set_taps(cw_model *m, int enable);
+/* Copy the tap `name` of `layer` from the last decode step to host (len
+ * floats; synchronises).  CW_ERR_STATE while taps are off. */
+int cw_model_tap(cw_model *m, const char *name, int layer, float *host_out, int len);
 /* How a decode step is executed (cw_generate, cw_model_decode_async). */
 #define CW_STEP_EAGER 0  /* 2 + 6*n_layers kernel launches per token */
 #define CW_STEP_GRAPH 1  /* the same launches captured once as a HIP graph and replayed */

@@ -704,9 +704,12 @@ static void gemv(const or_q4 *w, const float *x, int in_f, int out_f, float *y) 
 
 /* One token: embed (qwen3.rs:128-133), forward (qwen3.rs:139-191), logits
  * (qwen3.rs:135-137).  Writes logits[vocab]; optionally the final hidden
- * state and the per-layer "layer_out" taps (qwen3.rs:188). */
-OR_API void or_model_step(or_model *m, uint32_t tok, int pos, float *logits, float *hidden_out,
-                          float *layer_out) {
+ * state and the per-layer hook taps: "q" after QK-norm and RoPE
+ * (qwen3.rs:165), "post_attn" after the attention residual (qwen3.rs:180) and
+ * "layer_out" (qwen3.rs:188), each [n_layers][len]. */
+OR_API void or_model_step_taps(or_model *m, uint32_t tok, int pos, float *logits,
+                               float *hidden_out, float *q_tap, float *post_attn,
+                               float *layer_out) {
     int dim = m->dim, hd = m->head_dim, nh = m->n_heads, nkv = m->n_kv;
     int qd = nh * hd, kvd = nkv * hd, hid = m->hidden;
     float *hidden = (float *)malloc(sizeof(float) * dim);
@@ -735,6 +738,7 @@ OR_API void or_model_step(or_model *m, uint32_t tok, int pos, float *logits, flo
         or_rope(t, nh, hd, pos, m->cos_t, m->sin_t, q);
         or_rmsnorm(k, l->norm[OR_T_K_NORM], nkv, hd, m->eps, t);
         or_rope(t, nkv, hd, pos, m->cos_t, m->sin_t, k);
+        if (q_tap) memcpy(q_tap + (size_t)i * qd, q, sizeof(float) * qd);
         /* cache.write (cache.rs:21-24) */
         size_t off = ((size_t)i * m->max_seq + pos) * kvd;
         if (m->kv_f16) {
@@ -751,6 +755,7 @@ OR_API void or_model_step(or_model *m, uint32_t tok, int pos, float *logits, flo
         or_attention(q, kl, vl, m->kv_f16, nh, nkv, pos + 1, hd, attn);
         gemv(&l->w[OR_T_WO - OR_T_WQ], attn, qd, dim, tmp);
         or_add(hidden, tmp, dim, hidden);
+        if (post_attn) memcpy(post_attn + (size_t)i * dim, hidden, sizeof(float) * dim);
         or_rmsnorm(hidden, l->norm[OR_T_FFN_NORM], 1, dim, m->eps, normed);
         gemv(&l->w[OR_T_GATE - OR_T_WQ], normed, dim, hid, gate);
         gemv(&l->w[OR_T_UP - OR_T_WQ], normed, dim, hid, up);
@@ -764,6 +769,11 @@ OR_API void or_model_step(or_model *m, uint32_t tok, int pos, float *logits, flo
     if (logits) gemv(&m->lm_head, normed, dim, m->vocab, logits);
     free(hidden); free(normed); free(q); free(k); free(v); free(t); free(attn);
     free(tmp); free(gate); free(up); free(act); free(zero);
+}
+
+OR_API void or_model_step(or_model *m, uint32_t tok, int pos, float *logits, float *hidden_out,
+                          float *layer_out) {
+    or_model_step_taps(m, tok, pos, logits, hidden_out, NULL, NULL, layer_out);
 }
 
 /* mod.rs:57-125: greedy loop.  Position pos feeds prompt[pos] while inside

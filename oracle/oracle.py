@@ -50,6 +50,7 @@ _SIGS = {
     "or_model_set_globals": (None, [_P, _P, _P, _P, _P]),
     "or_model_prefill_kv": (None, [_P, _P, _P, _I]),
     "or_model_step": (None, [_P, C.c_uint32, _I, _P, _P, _P]),
+    "or_model_step_taps": (None, [_P, C.c_uint32, _I, _P, _P, _P, _P, _P]),
     "or_generate": (_I, [_P, _P, _I, _I, _I, _P, _P]),
     "or_set_threads": (None, [_I]),
     "or_get_threads": (_I, []),
@@ -454,6 +455,19 @@ class OracleModel:
         lib().or_model_step(self.h, int(token), int(pos), _p(logits), _p(hidden),
                             _p(layers) if want_layers else None)
         return (logits, hidden, layers) if want_layers else (logits, hidden)
+
+    def step_taps(self, token, pos):
+        """One token with the forward's hook taps (qwen3.rs:165,180,188):
+        (logits, {"q": [L][n_heads*hd], "post_attn": [L][dim],
+        "layer_out": [L][dim]})."""
+        c = self.cfg
+        logits = np.empty(c.vocab, np.float32)
+        taps = {"q": np.empty((c.n_layers, c.n_heads * c.head_dim), np.float32),
+                "post_attn": np.empty((c.n_layers, c.dim), np.float32),
+                "layer_out": np.empty((c.n_layers, c.dim), np.float32)}
+        lib().or_model_step_taps(self.h, int(token), int(pos), _p(logits), None, _p(taps["q"]),
+                                 _p(taps["post_attn"]), _p(taps["layer_out"]))
+        return logits, taps
 
     def generate(self, prompt, max_new, start_pos=0):
         prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
