@@ -97,8 +97,18 @@ float f16_bits_to_f32(uint16_t h) {
     return f;
 }
 
+// What would allocate or synchronise cannot run while a graph is being
+// recorded: the first use at a size must come before cw_graph_begin.
+static int refuse_while_capturing(const cw_ctx *ctx, const char *what) {
+    if (!ctx->capturing) return CW_OK;
+    set_error("%s while a graph is being recorded: run the sequence once before cw_graph_begin",
+              what);
+    return CW_ERR_STATE;
+}
+
 int ctx_scratch(cw_ctx *ctx, size_t bytes, void **out) {
     if (bytes > ctx->scratch_size) {
+        CW_TRY(refuse_while_capturing(ctx, "kernel scratch must grow"));
         CW_HIP(hipStreamSynchronize(ctx->stream));
         if (ctx->scratch) CW_HIP(hipFree(ctx->scratch));
         ctx->scratch = nullptr;
@@ -131,6 +141,7 @@ int ctx_rope_table(cw_ctx *ctx, float theta, int head_dim, int min_pos, const cw
             return CW_OK;
         }
     }
+    CW_TRY(refuse_while_capturing(ctx, "a RoPE table must be built"));
     int max_pos = 1024;
     while (max_pos < min_pos) max_pos *= 2;
     size_t n = (size_t)max_pos * (head_dim / 2);
@@ -288,6 +299,7 @@ int cw_frame_alloc(cw_ctx *ctx, size_t bytes, void **out) {
         ctx->chunk_idx++;
         ctx->chunk_off = 0;
     }
+    CW_TRY(refuse_while_capturing(ctx, "the frame arena must grow"));
     size_t sz = need < (64u << 20) ? (64u << 20) : need;
     cw_ctx::Chunk c{nullptr, sz};
     CW_HIP(hipMalloc((void **)&c.base, sz));
@@ -307,6 +319,7 @@ int cw_frame_reset(cw_ctx *ctx) {
 
 int cw_upload(cw_ctx *ctx, void *dst, const void *src, size_t bytes) {
     CW_CHECK_ARG(ctx && dst && src, "cw_upload: null argument");
+    CW_TRY(refuse_while_capturing(ctx, "cw_upload"));
     if (!bytes) return CW_OK;
     CW_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
     // the source is pageable host memory owned by the caller: finish before
@@ -317,6 +330,7 @@ int cw_upload(cw_ctx *ctx, void *dst, const void *src, size_t bytes) {
 
 int cw_download(cw_ctx *ctx, void *dst, const void *src, size_t bytes) {
     CW_CHECK_ARG(ctx && dst && src, "cw_download: null argument");
+    CW_TRY(refuse_while_capturing(ctx, "cw_download"));
     if (!bytes) return CW_OK;
     CW_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
     CW_HIP(hipStreamSynchronize(ctx->stream));
@@ -332,12 +346,14 @@ int cw_copy(cw_ctx *ctx, void *dst, const void *src, size_t bytes) {
 
 int cw_flush(cw_ctx *ctx) {
     CW_CHECK_ARG(ctx != nullptr, "cw_flush: null ctx");
+    CW_TRY(refuse_while_capturing(ctx, "cw_flush"));
     CW_HIP(hipStreamSynchronize(ctx->stream));
     return CW_OK;
 }
 
 int cw_profile_begin(cw_ctx *ctx) {
     CW_CHECK_ARG(ctx != nullptr, "cw_profile_begin: null ctx");
+    CW_TRY(refuse_while_capturing(ctx, "cw_profile_begin"));
     ctx->profiling = true;
     ctx->prof.clear();
     ctx->event_next = 0;
@@ -373,6 +389,65 @@ int cw_profile_report(cw_ctx *ctx, char *buf, size_t buf_len) {
         out += line;
     }
     snprintf(buf, buf_len, "%s", out.c_str());
+    return CW_OK;
+}
+
+struct cw_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+int cw_graph_begin(cw_ctx *ctx) {
+    CW_CHECK_ARG(ctx != nullptr, "cw_graph_begin: null ctx");
+    if (ctx->capturing || ctx->profiling) {
+        set_error("cw_graph_begin: %s", ctx->capturing ? "a recording is already open"
+                                                       : "profiling is on (cw_profile_report first)");
+        return CW_ERR_STATE;
+    }
+    CW_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeRelaxed));
+    ctx->capturing = true;
+    return CW_OK;
+}
+
+int cw_graph_end(cw_ctx *ctx, cw_graph **out) {
+    CW_CHECK_ARG(ctx && out, "cw_graph_end: null argument");
+    *out = nullptr;
+    if (!ctx->capturing) {
+        set_error("cw_graph_end: no recording is open (cw_graph_begin)");
+        return CW_ERR_STATE;
+    }
+    ctx->capturing = false;
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
+    if (e != hipSuccess) {
+        if (graph) hipGraphDestroy(graph);
+        return hip_fail(e, "hipStreamEndCapture", __FILE__, __LINE__);
+    }
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        hipGraphDestroy(graph);
+        return hip_fail(e, "hipGraphInstantiate", __FILE__, __LINE__);
+    }
+    cw_graph *g = new cw_graph();
+    g->graph = graph;
+    g->exec = exec;
+    *out = g;
+    return CW_OK;
+}
+
+int cw_graph_launch(cw_ctx *ctx, const cw_graph *g) {
+    CW_CHECK_ARG(ctx && g, "cw_graph_launch: null argument");
+    CW_TRY(refuse_while_capturing(ctx, "cw_graph_launch"));
+    CW_HIP(hipGraphLaunch(g->exec, ctx->stream));
+    return CW_OK;
+}
+
+int cw_graph_destroy(cw_graph *g) {
+    if (!g) return CW_OK;
+    if (g->exec) hipGraphExecDestroy(g->exec);
+    if (g->graph) hipGraphDestroy(g->graph);
+    delete g;
     return CW_OK;
 }
 

@@ -106,6 +106,9 @@ struct cw_ctx {
 
     std::vector<cw_rope_tab> ropes;
 
+    // a cw_graph_begin .. cw_graph_end recording is open on the stream
+    bool capturing = false;
+
     // profiling
     bool profiling = false;
     std::vector<cw_prof_rec> prof;

@@ -62,6 +62,10 @@ _SIGS = {
     "cw_download": (_I, [_P, _P, _P, _SZ]),
     "cw_copy": (_I, [_P, _P, _P, _SZ]),
     "cw_flush": (_I, [_P]),
+    "cw_graph_begin": (_I, [_P]),
+    "cw_graph_end": (_I, [_P, C.POINTER(_P)]),
+    "cw_graph_launch": (_I, [_P, _P]),
+    "cw_graph_destroy": (_I, [_P]),
     "cw_q4_gemv": (_I, [_P, _P, _P, _P, _I, _I, _P]),
     "cw_q4_gemv_add": (_I, [_P, _P, _P, _P, _I, _I, _P, _P]),
     "cw_q4_gemv_swiglu": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _P]),
@@ -316,6 +320,21 @@ class DeviceArray:
         return out
 
 
+class Graph:
+    """A recorded launch sequence of a Context (cw_graph_*)."""
+
+    def __init__(self, ctx, h):
+        self.ctx, self.h = ctx, h
+
+    def launch(self):
+        check(lib().cw_graph_launch(self.ctx.h, self.h))
+
+    def close(self):
+        if self.h:
+            lib().cw_graph_destroy(self.h)
+            self.h = None
+
+
 class Context:
     """GpuContext (src/context.rs): one HIP stream on one device."""
 
@@ -433,6 +452,16 @@ class Context:
         o = self.empty(dim)
         check(lib().cw_embed(self.h, table.ptr, vocab, dim, token_dev.ptr, o.ptr))
         return o
+
+    def graph_begin(self):
+        """Record the following launches (cw_graph_begin)."""
+        check(lib().cw_graph_begin(self.h))
+
+    def graph_end(self):
+        """Close the recording; returns a Graph to replay."""
+        g = _P()
+        check(lib().cw_graph_end(self.h, C.byref(g)))
+        return Graph(self, g.value)
 
     def hbm_read_probe(self, buf, nbytes, blocks, out):
         check(lib().cw_hbm_read_probe(self.h, buf.ptr, nbytes, blocks, out.ptr))

@@ -39,6 +39,7 @@ extern "C" {
 typedef struct cw_ctx cw_ctx;
 typedef struct cw_model cw_model;
 typedef struct cw_gguf cw_gguf;
+typedef struct cw_graph cw_graph;
 
 /* ---------------------------------------------------------------- */
 /* Context: device, stream, arena (src/context.rs)                   */
@@ -75,6 +76,23 @@ int cw_download(cw_ctx *ctx, void *dst_host, const void *src_dev, size_t bytes);
 int cw_copy(cw_ctx *ctx, void *dst_dev, const void *src_dev, size_t bytes);
 /* GpuContext::flush (src/context.rs:141-151): wait until the stream drains. */
 int cw_flush(cw_ctx *ctx);
+
+/* Recorded launch sequences: the counterpart of the reference's per-frame
+ * command-buffer replay, whose bind-group cache needs the same op sequence
+ * every frame (src/context.rs:141-151, 330-334).  cw_graph_begin starts
+ * recording the context's kernel launches instead of running them;
+ * cw_graph_end closes the recording into an executable graph; cw_graph_launch
+ * replays it on the stream (the buffers, shapes and scalars recorded stay
+ * fixed; device-resident values, such as a position read by a kernel, may
+ * change between replays); cw_graph_destroy frees it.  While recording, calls
+ * that would allocate or synchronise fail with CW_ERR_STATE (uploads,
+ * downloads, flush, profiling, a first frame-arena chunk, kernel scratch or
+ * RoPE table at a new size): run the sequence once before recording.  The
+ * cw_model_* calls keep their own graph and are not recordable. */
+int cw_graph_begin(cw_ctx *ctx);
+int cw_graph_end(cw_ctx *ctx, cw_graph **out);
+int cw_graph_launch(cw_ctx *ctx, const cw_graph *g);
+int cw_graph_destroy(cw_graph *g);
 
 /* ---------------------------------------------------------------- */
 /* Kernels (src/kernels/NAME.rs).  Q4 weights are GGUF Q4_0 split into   */
