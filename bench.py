@@ -294,7 +294,7 @@ def main():
                          "print only the 512-token prefill figures (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
+        print(json.dumps({"error": "this library runs on one GPU; --gpus must be 1 "
                           "(no multi-GPU path is built)"}))
         sys.exit(2)
     K, W = args.steps, args.warmup

@@ -492,7 +492,7 @@ __device__ __forceinline__ KVT to_kv(float v) {
     return (KVT)v;  // f16: round to nearest even
 }
 
-// Issue the K/V tile loads of this thread's item in round 0.
+// Issue the K/V tile loads of this thread's item in the first pass.
 template <typename KVT, int HPK>
 __device__ __forceinline__ void attn_load(const StepArgs &a, const StepLayer &L, const AttnGeo &g,
                                           int item, uint4 (&rq)[kQ]) {

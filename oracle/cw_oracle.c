@@ -1,9 +1,10 @@
 /*
  * cw_oracle.c -- CPU restatement of chat-wgpu's decode token loop.
  *
- * TEST INFRASTRUCTURE ONLY.  This file is the checker: only tests/,
- * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.  The
- * product (chat-wgpu_amd/) never links or calls it.
+ * TEST INFRASTRUCTURE ONLY.  This file is the oracle the device results are
+ * compared with: only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it.  The product (chat-wgpu_amd/) never links or
+ * calls it.
  *
  * Every function restates one piece of the reference (Rust + WGSL), cited as
  * file:line relative to the reference repository root.  Arithmetic is plain

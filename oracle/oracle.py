@@ -1,7 +1,8 @@
 """ctypes wrapper of oracle/liboracle.so -- the CPU restatement of the reference.
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
-bench.py's cpu_baseline leg, as the checker.  The product never imports it.
+bench.py's cpu_baseline leg, as what the device results are checked against.
+The product never imports it.
 """
 import ctypes as C
 import os

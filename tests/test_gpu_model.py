@@ -1,8 +1,8 @@
 """Token-loop parity on the MI355X: the device-resident Qwen3 decode loop
 (HIP graph replay) against the CPU oracle's forward/generate.
 
-Bars: greedy token ids identical over the horizon;
-teacher-forced logits within 1e-3 absolute at every step.
+Bars: greedy token ids identical over the horizon; teacher-forced logits
+within 1e-3 absolute at every step.
 """
 import os
 
