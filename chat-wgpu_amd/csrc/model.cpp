@@ -460,8 +460,17 @@ int pf_linear(cw_model *m, const float *x, const float *norm_w, int n, int K, Ep
     return launch_q4_gemm(m->ctx, epi, a);
 }
 
+// With taps on: row `row` of a batched [n][floats] buffer into a tap.
+int tap_row(cw_model *m, float *dst, const float *src, int row, int floats) {
+    if (!m->taps) return CW_OK;
+    CW_HIP(hipMemcpyAsync(dst, src + (size_t)row * floats, (size_t)floats * 4,
+                          hipMemcpyDeviceToDevice, m->ctx->stream));
+    return CW_OK;
+}
+
 // Forward of n positions start..start+n-1 (tokens in m->prompt_dev) through
 // every layer with the batched kernels; leaves the hidden rows in pf_hidden.
+// With taps on, the taps are those of the last position's forward.
 int enqueue_prefill(cw_model *m, int n, int start) {
     cw_ctx *ctx = m->ctx;
     const auto &c = m->cfg;
@@ -474,14 +483,17 @@ int enqueue_prefill(cw_model *m, int n, int start) {
                          nullptr, m->pf_qkv));
         CW_TRY(launch_qk_rope_kv(ctx, m->pf_qkv, L.q_norm, L.k_norm, c.eps, m->cos_t, m->sin_t, n,
                                  c.n_heads, c.n_kv_heads, start, c.kv_dtype, m->pf_q, kc, vc));
+        CW_TRY(tap_row(m, m->tap_q + (size_t)i * m->q_dim, m->pf_q, n - 1, m->q_dim));
         CW_TRY(launch_attn_prefill(ctx, m->pf_q, kc, vc, n, c.n_heads, c.n_kv_heads, start,
                                    m->pf_attn));
         CW_TRY(pf_linear(m, m->pf_attn, nullptr, n, m->q_dim, EPI_ADD, L.wo, nullptr,
                          m->pf_hidden, m->pf_hidden));
+        CW_TRY(tap_row(m, m->tap_post + (size_t)i * c.dim, m->pf_hidden, n - 1, c.dim));
         CW_TRY(pf_linear(m, m->pf_hidden, L.ffn_norm, n, c.dim, EPI_SWIGLU, L.gate, &L.up,
                          nullptr, m->pf_act));
         CW_TRY(pf_linear(m, m->pf_act, nullptr, n, c.hidden, EPI_ADD, L.down, nullptr,
                          m->pf_hidden, m->pf_hidden));
+        CW_TRY(tap_row(m, m->tap_out + (size_t)i * c.dim, m->pf_hidden, n - 1, c.dim));
     }
     return CW_OK;
 }

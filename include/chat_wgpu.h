@@ -239,7 +239,7 @@ int cw_model_hidden(cw_model *m, float *host_out);
  * (qwen3.rs:165, n_heads*head_dim floats), "post_attn" after the attention
  * residual (qwen3.rs:180, dim floats) and "layer_out" (qwen3.rs:188, dim
  * floats).  Toggling re-captures the graph step; the batched prompt phase
- * records no taps. */
+ * (cw_model_prefill) records the taps of its last position. */
 int cw_model_set_taps(cw_model *m, int enable);
 /* Copy the tap `name` of `layer` from the last decode step to host (len
  * floats; synchronises).  CW_ERR_STATE while taps are off. */

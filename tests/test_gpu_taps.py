@@ -94,3 +94,19 @@ def test_taps_leave_results_unchanged_and_errors(ctx):
     assert np.array_equal(toks_off, toks_on)
     m.close()
     o.close()
+
+
+def test_taps_of_batched_prompt_phase(ctx):
+    """cw_model_prefill with taps on leaves the taps of the last prompt
+    position's forward, as the per-token loop's last step would."""
+    P = 20
+    m, o = build(ctx, small(P + 2), 64)
+    m.set_taps(True)
+    prompt = cw.synth_tokens(cw.synth_key(64, "prompt"), P, m.cfg.vocab)
+    m.prefill(prompt)
+    for pos, t in enumerate(prompt[:-1]):
+        o.step(int(t), pos)
+    _, taps = o.step_taps(int(prompt[-1]), P - 1)
+    check_taps(m, taps, "prefill")
+    m.close()
+    o.close()
