@@ -16,6 +16,9 @@ maps it to ids and back, and decides when to stop.
 """
 from tokenizers import Tokenizer
 
+# cw.STEP_GRAPH: a decode step replayed from its captured HIP graph
+STEP_GRAPH = 1
+
 # end-of-turn markers looked up in the tokenizer's vocabulary (wasm.rs:48-51)
 EOS_TOKENS = ("<|im_end|>", "<|endoftext|>")
 
@@ -91,6 +94,10 @@ class LocalChat:
         else:
             for pos, t in enumerate(ids):
                 nxt = self.model.step(t, pos)
+        # after the batched prompt phase the decode state lives on the device:
+        # each further token is one replay of the captured step (the
+        # benchmarked path), read back as the device loop's newest id
+        graph = batched_prefill and hasattr(self.model, "decode_async")
         pos = len(ids)
         produced, shown = [], ""
         for i in range(max_tokens):
@@ -104,7 +111,11 @@ class LocalChat:
                     on_token(piece)
                 shown = full
             if i + 1 < max_tokens:  # the step after the last token would be unused
-                nxt = self.model.step(nxt, pos)
+                if graph:
+                    self.model.decode_async(1, mode=STEP_GRAPH)
+                    nxt = int(self.model.tokens(i + 1)[-1])
+                else:
+                    nxt = self.model.step(nxt, pos)
                 pos += 1
         self.last_reply_ids = produced
         return shown
