@@ -15,7 +15,9 @@
 //      query broadcast from LDS (f16 keys feed v_fma_mix directly) while the
 //      V rows are still arriving; wavefront max / sum give the chunk's
 //      softmax partial;
-//   3. wave j: lane = head dimension, P.V over the V tile's rows.
+//   3. wave j: lane = head dimension, P.V over its 1/HPK of the V tile's rows
+//      for every head of the group (each V row leaves LDS once), the waves'
+//      sums added through LDS.
 // No cross-lane reduction is needed per position.  A chunk partial
 // (max, sum, unnormalised o) goes to memory unless the sequence fits one
 // chunk, in which case the normalised output is written directly.  The last
@@ -82,6 +84,8 @@ struct Cfg {
     static constexpr int MB = MB0 < 18 ? MB0 : 18;
     static_assert(LDS <= 160 * 1024, "attention tile exceeds the CU's LDS");
     static_assert(CP >= 8 && CP % 8 == 0, "chunk must hold whole load groups");
+    static_assert((CP / HPK) % 4 == 0, "every wave's P.V rows come in fours");
+    static_assert(HPK * HPK * HD * 4 <= CP * ROWP, "P.V sums must fit the K tile");
 };
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -404,22 +408,25 @@ __global__ __launch_bounds__(64 * HPK) void attn_kernel(cwi::AttnArgs a, float s
         __syncthreads();
     }
 
-    // ---- 5. P.V: lane = head dimension, every tile row (masked rows carry
-    // p = 0 and a finite clamped V row), unrolled so LDS reads batch up ----
+    // ---- 5. P.V: lane = head dimension.  One head: the wave runs over
+    // every tile row.  A head group: wave w takes CP / HPK consecutive rows
+    // for all HPK heads, so each V row is read from LDS once (not once per
+    // head), and the per-wave sums meet in the K tile's space, which no wave
+    // reads after the barrier above.  Masked rows carry p = 0 and a finite
+    // clamped V row; loops are unrolled so LDS reads batch up ----
     float o[C::DPL];
     const int d0 = lane * C::DPL;
-    {
+    if constexpr (HPK == 1) {
         float o4[C::DPL][4];  // independent partial sums over rows
 #pragma unroll
         for (int e = 0; e < C::DPL; ++e)
 #pragma unroll
             for (int j = 0; j < 4; ++j) o4[e][j] = 0.0f;
         if (d0 < HD) {
-            const float *pw = p_s + wave * C::CP;
 #pragma unroll
             for (int r0 = 0; r0 < C::CP; r0 += 8) {
-                const float4 pa = *reinterpret_cast<const float4 *>(pw + r0);
-                const float4 pb = *reinterpret_cast<const float4 *>(pw + r0 + 4);
+                const float4 pa = *reinterpret_cast<const float4 *>(p_s + r0);
+                const float4 pb = *reinterpret_cast<const float4 *>(p_s + r0 + 4);
                 const float pr[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
@@ -432,6 +439,67 @@ __global__ __launch_bounds__(64 * HPK) void attn_kernel(cwi::AttnArgs a, float s
         }
 #pragma unroll
         for (int e = 0; e < C::DPL; ++e) o[e] = (o4[e][0] + o4[e][1]) + (o4[e][2] + o4[e][3]);
+    } else {
+        constexpr int RPW = C::CP / HPK;                  // rows per wave
+        constexpr int NS = HPK * C::DPL >= 8 ? 1 : 2;    // partial sums per output
+        float acc[HPK][C::DPL][NS];
+#pragma unroll
+        for (int hh = 0; hh < HPK; ++hh)
+#pragma unroll
+            for (int e = 0; e < C::DPL; ++e)
+#pragma unroll
+                for (int j = 0; j < NS; ++j) acc[hh][e][j] = 0.0f;
+        const int rbase = wave * RPW;
+        if (d0 < HD) {
+#pragma unroll
+            for (int r0 = 0; r0 < RPW; r0 += 4) {
+                float pr[HPK][4];
+#pragma unroll
+                for (int hh = 0; hh < HPK; ++hh) {
+                    const float4 p4 =
+                        *reinterpret_cast<const float4 *>(p_s + hh * C::CP + rbase + r0);
+                    pr[hh][0] = p4.x;
+                    pr[hh][1] = p4.y;
+                    pr[hh][2] = p4.z;
+                    pr[hh][3] = p4.w;
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const KVT *vrow =
+                        reinterpret_cast<const KVT *>(v_t + (rbase + r0 + i) * C::ROWP) + d0;
+                    float vv[C::DPL];
+#pragma unroll
+                    for (int e = 0; e < C::DPL; ++e) vv[e] = (float)vrow[e];
+#pragma unroll
+                    for (int hh = 0; hh < HPK; ++hh)
+#pragma unroll
+                        for (int e = 0; e < C::DPL; ++e)
+                            acc[hh][e][i % NS] =
+                                __builtin_fmaf(pr[hh][i], vv[e], acc[hh][e][i % NS]);
+                }
+            }
+        }
+        float *red = reinterpret_cast<float *>(k_t);  // [wave][head][HD]
+        if (d0 < HD) {
+#pragma unroll
+            for (int hh = 0; hh < HPK; ++hh)
+#pragma unroll
+                for (int e = 0; e < C::DPL; ++e) {
+                    float t = acc[hh][e][0];
+#pragma unroll
+                    for (int j = 1; j < NS; ++j) t += acc[hh][e][j];
+                    red[(wave * HPK + hh) * HD + d0 + e] = t;
+                }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < C::DPL; ++e) o[e] = 0.0f;
+        if (d0 < HD) {
+#pragma unroll
+            for (int w = 0; w < HPK; ++w)
+#pragma unroll
+                for (int e = 0; e < C::DPL; ++e) o[e] += red[(w * HPK + wave) * HD + d0 + e];
+        }
     }
 
     // ---- 6. output (one chunk) or chunk partial (h: this wave's head) ----
