@@ -114,8 +114,8 @@ int ctx_scratch(cw_ctx *ctx, size_t bytes, void **out) {
         ctx->scratch = nullptr;
         size_t sz = bytes < (1u << 20) ? (1u << 20) : bytes;
         CW_HIP(hipMalloc(&ctx->scratch, sz));
-        // counters inside scratch must start at zero
-        CW_HIP(hipMemset(ctx->scratch, 0, sz));
+        // counters inside scratch must start at zero (cleared in stream order)
+        CW_HIP(hipMemsetAsync(ctx->scratch, 0, sz, ctx->stream));
         ctx->scratch_size = sz;
     }
     *out = ctx->scratch;

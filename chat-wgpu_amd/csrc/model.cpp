@@ -100,6 +100,14 @@ namespace {
 // launch it returns CW_ERR_STATE instead.
 constexpr bool kFusedStepDisabled = true;
 
+// Model calls synchronise, allocate or clear memory, none of which may be
+// recorded into a caller's launch sequence (cw_graph_begin .. cw_graph_end).
+int refuse_recording(const cw_model *m, const char *what) {
+    if (!m->ctx->capturing) return CW_OK;
+    set_error("%s: not allowed while a graph is being recorded (end it with cw_graph_end)", what);
+    return CW_ERR_STATE;
+}
+
 int dalloc(cw_model *m, size_t bytes, void **out) {
     void *p = nullptr;
     CW_HIP(hipMalloc(&p, bytes));
@@ -119,9 +127,8 @@ int alloc_q4(cw_model *m, Q4W &w, int out_f, int in_f) {
 
 int upload_rows(cw_model *m, Q4W &w, int row0, int rows, const uint16_t *s, const uint8_t *q) {
     const size_t nb = w.in_f / 32;
-    CW_HIP(hipMemcpy(w.s + (size_t)row0 * nb, s, (size_t)rows * nb * 2, hipMemcpyHostToDevice));
-    CW_HIP(hipMemcpy(w.q + (size_t)row0 * nb * 16, q, (size_t)rows * nb * 16, hipMemcpyHostToDevice));
-    (void)m;
+    CW_TRY(cw_upload(m->ctx, w.s + (size_t)row0 * nb, s, (size_t)rows * nb * 2));
+    CW_TRY(cw_upload(m->ctx, w.q + (size_t)row0 * nb * 16, q, (size_t)rows * nb * 16));
     return CW_OK;
 }
 
@@ -285,7 +292,7 @@ int check_fused(cw_model *m) {
                           m->ctx->stream));
     CW_HIP(hipStreamSynchronize(m->ctx->stream));
     if (err) {
-        CW_HIP(hipMemset(m->step_sync, 0, step_sync_words() * 4));
+        CW_HIP(hipMemsetAsync(m->step_sync, 0, step_sync_words() * 4, m->ctx->stream));
         set_error(err == 2 ? "decode step: position outside the KV cache (launch skipped)"
                            : "decode step: a grid barrier timed out (launch abandoned)");
         return CW_ERR_HIP;
@@ -350,7 +357,7 @@ int setup_fused(cw_model *m) {
     }
     StepArgs &a = m->step;
     CW_TRY(dalloc(m, sizeof(StepLayer) * L, (void **)&m->step_layers));
-    CW_HIP(hipMemcpy(m->step_layers, host.data(), sizeof(StepLayer) * L, hipMemcpyHostToDevice));
+    CW_TRY(cw_upload(m->ctx, m->step_layers, host.data(), sizeof(StepLayer) * L));
     const int max_chunks = (c.max_seq + 7) / 8;
     CW_TRY(dalloc(m, (size_t)(L + 1) * c.dim * 4, (void **)&a.h_a));
     CW_TRY(dalloc(m, (size_t)L * c.dim * 4, (void **)&a.h_b));
@@ -361,7 +368,7 @@ int setup_fused(cw_model *m) {
     CW_TRY(dalloc(m, (size_t)m->ctx->n_cu * 4, (void **)&a.am_v));
     CW_TRY(dalloc(m, (size_t)m->ctx->n_cu * 4, (void **)&a.am_i));
     CW_TRY(dalloc(m, step_sync_words() * 4, (void **)&m->step_sync));
-    CW_HIP(hipMemset(m->step_sync, 0, step_sync_words() * 4));
+    CW_HIP(hipMemsetAsync(m->step_sync, 0, step_sync_words() * 4, m->ctx->stream));
     int rate_khz = 0;
     CW_HIP(hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, m->ctx->device));
     if (rate_khz <= 0) rate_khz = 100000;
@@ -392,7 +399,7 @@ int setup_fused(cw_model *m) {
     a.timeout = (long long)rate_khz * 1000 * 2;  // 2 s
     a.trace = nullptr;
     CW_TRY(dalloc(m, sizeof(StepArgs), (void **)&m->step_dev));
-    CW_HIP(hipMemcpy(m->step_dev, &a, sizeof(StepArgs), hipMemcpyHostToDevice));
+    CW_TRY(cw_upload(m->ctx, m->step_dev, &a, sizeof(StepArgs)));
     return CW_OK;
 }
 
@@ -519,6 +526,11 @@ extern "C" {
 int cw_model_create(cw_ctx *ctx, const cw_model_config *cfg, cw_model **out) {
     CW_CHECK_ARG(ctx && cfg && out, "cw_model_create: null argument");
     *out = nullptr;
+    if (ctx->capturing) {
+        set_error("cw_model_create: not allowed while a graph is being recorded (end it with "
+                  "cw_graph_end)");
+        return CW_ERR_STATE;
+    }
     const auto &c = *cfg;
     CW_CHECK_ARG(c.family.norm_unit_gain == 0 && c.family.act == 0 && c.family.qk_norm == 1 &&
                      c.family.qkv_bias == 0,
@@ -587,9 +599,10 @@ int cw_model_create(cw_ctx *ctx, const cw_model_config *cfg, cw_model **out) {
         (rc = dalloc(m, 4, (void **)&m->argmax_out)))
         return fail(rc);
     // zero the caches so positions never written read as 0, not garbage
-    if (hipMemset(m->kcache, 0, m->kv_layer_bytes * c.n_layers) != hipSuccess ||
-        hipMemset(m->vcache, 0, m->kv_layer_bytes * c.n_layers) != hipSuccess) {
-        set_error("cw_model_create: hipMemset of the KV cache failed");
+    // cleared on the context stream, so every later copy and launch is ordered after
+    if (hipMemsetAsync(m->kcache, 0, m->kv_layer_bytes * c.n_layers, ctx->stream) != hipSuccess ||
+        hipMemsetAsync(m->vcache, 0, m->kv_layer_bytes * c.n_layers, ctx->stream) != hipSuccess) {
+        set_error("cw_model_create: clearing the KV cache failed");
         return fail(CW_ERR_HIP);
     }
     const cw_rope_tab *t = nullptr;
@@ -602,6 +615,7 @@ int cw_model_create(cw_ctx *ctx, const cw_model_config *cfg, cw_model **out) {
 
 int cw_model_destroy(cw_model *m) {
     if (!m) return CW_OK;
+    CW_TRY(refuse_recording(m, "cw_model_destroy"));
     hipStreamSynchronize(m->ctx->stream);
     if (m->graph_exec) hipGraphExecDestroy(m->graph_exec);
     if (m->graph) hipGraphDestroy(m->graph);
@@ -613,6 +627,7 @@ int cw_model_destroy(cw_model *m) {
 
 int cw_model_set_q4(cw_model *m, const char *name, const uint16_t *scales, const uint8_t *quants) {
     CW_CHECK_ARG(m && name && scales && quants, "cw_model_set_q4: null argument");
+    CW_TRY(refuse_recording(m, "cw_model_set_q4"));
     if (strcmp(name, "output.weight") == 0) {
         CW_TRY(upload_rows(m, m->lm_head, 0, m->cfg.vocab, scales, quants));
         m->have_output = true;
@@ -647,14 +662,15 @@ int cw_model_set_q4(cw_model *m, const char *name, const uint16_t *scales, const
 
 int cw_model_set_f32(cw_model *m, const char *name, const float *data) {
     CW_CHECK_ARG(m && name && data, "cw_model_set_f32: null argument");
+    CW_TRY(refuse_recording(m, "cw_model_set_f32"));
     const auto &c = m->cfg;
     if (strcmp(name, "token_embd.weight") == 0) {
-        CW_HIP(hipMemcpy(m->embed, data, (size_t)c.vocab * c.dim * 4, hipMemcpyHostToDevice));
+        CW_TRY(cw_upload(m->ctx, m->embed, data, (size_t)c.vocab * c.dim * 4));
         m->have_embed = true;
         return CW_OK;
     }
     if (strcmp(name, "output_norm.weight") == 0) {
-        CW_HIP(hipMemcpy(m->final_norm, data, (size_t)c.dim * 4, hipMemcpyHostToDevice));
+        CW_TRY(cw_upload(m->ctx, m->final_norm, data, (size_t)c.dim * 4));
         m->have_final = true;
         return CW_OK;
     }
@@ -667,13 +683,14 @@ int cw_model_set_f32(cw_model *m, const char *name, const float *data) {
                  : id == T_K_NORM  ? L.k_norm
                                    : L.ffn_norm;
     const size_t n = (id == T_Q_NORM || id == T_K_NORM) ? c.head_dim : c.dim;
-    CW_HIP(hipMemcpy(dst, data, n * 4, hipMemcpyHostToDevice));
+    CW_TRY(cw_upload(m->ctx, dst, data, n * 4));
     m->have[li][id] = true;
     return CW_OK;
 }
 
 int cw_model_load_synthetic(cw_model *m, uint64_t seed) {
     CW_CHECK_ARG(m != nullptr, "cw_model_load_synthetic: null model");
+    CW_TRY(refuse_recording(m, "cw_model_load_synthetic"));
     const auto &c = m->cfg;
     std::vector<uint16_t> s;
     std::vector<uint8_t> q;
@@ -712,6 +729,7 @@ int cw_model_load_synthetic(cw_model *m, uint64_t seed) {
 
 int cw_model_load_gguf(cw_model *m, const cw_gguf *g) {
     CW_CHECK_ARG(m && g, "cw_model_load_gguf: null argument");
+    CW_TRY(refuse_recording(m, "cw_model_load_gguf"));
     const auto &c = m->cfg;
     std::vector<uint16_t> s;
     std::vector<uint8_t> q;
@@ -753,6 +771,7 @@ int cw_model_load_gguf(cw_model *m, const cw_gguf *g) {
 
 int cw_model_finalize(cw_model *m) {
     CW_CHECK_ARG(m != nullptr, "cw_model_finalize: null model");
+    CW_TRY(refuse_recording(m, "cw_model_finalize"));
     const auto &c = m->cfg;
     for (int i = 0; i < c.n_layers; ++i)
         for (int id = 0; id < T_N; ++id)
@@ -771,7 +790,7 @@ int cw_model_finalize(cw_model *m) {
     if (!m->have_output) {
         // tied LM head (qwen3.rs:93-98): re-quantize the f32 embedding
         std::vector<float> e((size_t)c.vocab * c.dim);
-        CW_HIP(hipMemcpy(e.data(), m->embed, e.size() * 4, hipMemcpyDeviceToHost));
+        CW_TRY(cw_download(m->ctx, e.data(), m->embed, e.size() * 4));
         const size_t nblk = (size_t)c.vocab * (c.dim / 32);
         std::vector<uint16_t> s(nblk);
         std::vector<uint8_t> q(nblk * 16);
@@ -785,21 +804,23 @@ int cw_model_finalize(cw_model *m) {
 
 int cw_model_prefill_kv(cw_model *m, const void *k, const void *v, int n_pos) {
     CW_CHECK_ARG(m && k && v, "cw_model_prefill_kv: null argument");
+    CW_TRY(refuse_recording(m, "cw_model_prefill_kv"));
     CW_CHECK_ARG(n_pos > 0 && n_pos <= m->cfg.max_seq, "cw_model_prefill_kv: n_pos=%d (max_seq %d)",
                  n_pos, m->cfg.max_seq);
     const size_t es = m->cfg.kv_dtype == CW_F16 ? 2 : 4;
     const size_t row = (size_t)n_pos * m->kv_dim * es;
     for (int l = 0; l < m->cfg.n_layers; ++l) {
-        CW_HIP(hipMemcpy((char *)m->kcache + l * m->kv_layer_bytes, (const char *)k + l * row, row,
-                         hipMemcpyHostToDevice));
-        CW_HIP(hipMemcpy((char *)m->vcache + l * m->kv_layer_bytes, (const char *)v + l * row, row,
-                         hipMemcpyHostToDevice));
+        CW_TRY(cw_upload(m->ctx, (char *)m->kcache + l * m->kv_layer_bytes,
+                         (const char *)k + l * row, row));
+        CW_TRY(cw_upload(m->ctx, (char *)m->vcache + l * m->kv_layer_bytes,
+                         (const char *)v + l * row, row));
     }
     return CW_OK;
 }
 
 int cw_model_step(cw_model *m, uint32_t token, int pos, uint32_t *argmax_out) {
     CW_CHECK_ARG(m != nullptr, "cw_model_step: null model");
+    CW_TRY(refuse_recording(m, "cw_model_step"));
     CW_TRY(require_final(m, "cw_model_step"));
     CW_CHECK_ARG(token < (uint32_t)m->cfg.vocab, "cw_model_step: token %u >= vocab %d", token,
                  m->cfg.vocab);
@@ -829,14 +850,21 @@ int cw_model_hidden(cw_model *m, float *host_out) {
 
 int cw_model_set_taps(cw_model *m, int enable) {
     CW_CHECK_ARG(m != nullptr, "cw_model_set_taps: null model");
+    CW_TRY(refuse_recording(m, "cw_model_set_taps"));
     const auto &c = m->cfg;
-    if (enable && !m->tap_q) {
-        CW_TRY(dalloc(m, (size_t)c.n_layers * m->q_dim * 4, (void **)&m->tap_q));
-        CW_TRY(dalloc(m, (size_t)c.n_layers * c.dim * 4, (void **)&m->tap_post));
-        CW_TRY(dalloc(m, (size_t)c.n_layers * c.dim * 4, (void **)&m->tap_out));
-        CW_HIP(hipMemsetAsync(m->tap_q, 0, (size_t)c.n_layers * m->q_dim * 4, m->ctx->stream));
-        CW_HIP(hipMemsetAsync(m->tap_post, 0, (size_t)c.n_layers * c.dim * 4, m->ctx->stream));
-        CW_HIP(hipMemsetAsync(m->tap_out, 0, (size_t)c.n_layers * c.dim * 4, m->ctx->stream));
+    if (enable) {
+        // each buffer is made (and cleared) once; a failed allocation leaves
+        // the taps off and the next call retries the missing ones
+        float **bufs[3] = {&m->tap_q, &m->tap_post, &m->tap_out};
+        const size_t floats[3] = {(size_t)c.n_layers * m->q_dim, (size_t)c.n_layers * c.dim,
+                                  (size_t)c.n_layers * c.dim};
+        for (int i = 0; i < 3; ++i) {
+            if (*bufs[i]) continue;
+            void *p = nullptr;
+            CW_TRY(dalloc(m, floats[i] * 4, &p));
+            CW_HIP(hipMemsetAsync(p, 0, floats[i] * 4, m->ctx->stream));
+            *bufs[i] = static_cast<float *>(p);
+        }
     }
     if ((enable != 0) != m->taps) {
         // the captured step holds the other buffer addresses: capture again
@@ -881,6 +909,7 @@ int cw_model_tap(cw_model *m, const char *name, int layer, float *host_out, int 
 int cw_generate(cw_model *m, const uint32_t *prompt, int n_prompt, int max_new, int start_pos,
                 int mode, uint32_t *out_tokens) {
     CW_CHECK_ARG(m && prompt && out_tokens, "cw_generate: null argument");
+    CW_TRY(refuse_recording(m, "cw_generate"));
     CW_TRY(require_final(m, "cw_generate"));
     CW_CHECK_ARG(n_prompt >= 1 && max_new >= 1, "cw_generate: n_prompt=%d max_new=%d", n_prompt,
                  max_new);
@@ -891,7 +920,7 @@ int cw_generate(cw_model *m, const uint32_t *prompt, int n_prompt, int max_new, 
     for (int i = 0; i < n_prompt; ++i)
         CW_CHECK_ARG(prompt[i] < (uint32_t)m->cfg.vocab, "cw_generate: prompt[%d]=%u >= vocab", i,
                      prompt[i]);
-    CW_HIP(hipMemcpy(m->prompt_dev, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice));
+    CW_TRY(cw_upload(m->ctx, m->prompt_dev, prompt, (size_t)n_prompt * 4));
     GenState s{start_pos, prompt[0], start_pos, n_prompt, 0, max_new};
     CW_TRY(set_state(m, s));
     CW_TRY(run_steps(m, (int)total, mode));
@@ -904,6 +933,7 @@ int cw_generate(cw_model *m, const uint32_t *prompt, int n_prompt, int max_new, 
 int cw_model_prefill(cw_model *m, const uint32_t *tokens, int n, int start_pos,
                      uint32_t *next_token) {
     CW_CHECK_ARG(m && tokens, "cw_model_prefill: null argument");
+    CW_TRY(refuse_recording(m, "cw_model_prefill"));
     CW_TRY(require_final(m, "cw_model_prefill"));
     const auto &c = m->cfg;
     CW_CHECK_ARG(n >= 1 && start_pos >= 0 && (long)start_pos + n <= c.max_seq,
@@ -912,7 +942,7 @@ int cw_model_prefill(cw_model *m, const uint32_t *tokens, int n, int start_pos,
     for (int i = 0; i < n; ++i)
         CW_CHECK_ARG(tokens[i] < (uint32_t)c.vocab, "cw_model_prefill: tokens[%d]=%u >= vocab", i,
                      tokens[i]);
-    CW_HIP(hipMemcpy(m->prompt_dev, tokens, (size_t)n * 4, hipMemcpyHostToDevice));
+    CW_TRY(cw_upload(m->ctx, m->prompt_dev, tokens, (size_t)n * 4));
     const bool batched = c.kv_dtype == CW_F16 && c.head_dim == 128;
     if (batched) {
         CW_TRY(ensure_prefill(m, n));
@@ -952,6 +982,7 @@ int cw_model_prefill(cw_model *m, const uint32_t *tokens, int n, int start_pos,
 
 int cw_model_reset_state(cw_model *m, uint32_t token, int pos) {
     CW_CHECK_ARG(m != nullptr, "cw_model_reset_state: null model");
+    CW_TRY(refuse_recording(m, "cw_model_reset_state"));
     CW_CHECK_ARG(token < (uint32_t)m->cfg.vocab && pos >= 0 && pos < m->cfg.max_seq,
                  "cw_model_reset_state: token=%u pos=%d", token, pos);
     GenState s{pos, token, pos, 1, 0, m->cfg.max_seq};
@@ -960,6 +991,7 @@ int cw_model_reset_state(cw_model *m, uint32_t token, int pos) {
 
 int cw_model_decode_async(cw_model *m, int n_steps, int mode) {
     CW_CHECK_ARG(m != nullptr && n_steps >= 0, "cw_model_decode_async: bad argument");
+    CW_TRY(refuse_recording(m, "cw_model_decode_async"));
     CW_TRY(require_final(m, "cw_model_decode_async"));
     GenState s{};
     CW_HIP(hipMemcpyAsync(&s, m->state, sizeof s, hipMemcpyDeviceToHost, m->ctx->stream));
@@ -972,6 +1004,7 @@ int cw_model_decode_async(cw_model *m, int n_steps, int mode) {
 
 int cw_model_profile_step(cw_model *m, int64_t *ticks, int max_n, int *n_out, double *tick_hz) {
     CW_CHECK_ARG(m && ticks && n_out && tick_hz, "cw_model_profile_step: null argument");
+    CW_TRY(refuse_recording(m, "cw_model_profile_step"));
     CW_TRY(require_final(m, "cw_model_profile_step"));
     if (kFusedStepDisabled) {
         set_error("fused decode step disabled (see CW_STEP_FUSED)");
@@ -1019,6 +1052,7 @@ int cw_model_profile_step(cw_model *m, int64_t *ticks, int max_n, int *n_out, do
 
 int cw_model_tokens(cw_model *m, uint32_t *host_out, int max_n, int *n_out) {
     CW_CHECK_ARG(m && host_out && n_out, "cw_model_tokens: null argument");
+    CW_TRY(refuse_recording(m, "cw_model_tokens"));
     CW_TRY(check_fused(m));
     GenState s{};
     CW_HIP(hipMemcpyAsync(&s, m->state, sizeof s, hipMemcpyDeviceToHost, m->ctx->stream));

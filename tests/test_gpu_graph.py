@@ -2,7 +2,7 @@
 per-frame replay, context.rs:141-151,330-334): a recorded sequence of kernel
 calls replayed several times, with eager uploads and synchronisation between
 the replays, gives exactly what the same calls give eagerly; calls that would
-allocate or synchronise are refused while recording."""
+allocate or synchronise, the model's among them, are refused while recording."""
 import numpy as np
 import pytest
 
@@ -78,3 +78,22 @@ def test_recording_refuses_a_first_allocation(ctx, rng):
                                 o.ptr))
     g = ctx.graph_end()
     g.close()
+
+
+def test_recording_refuses_model_calls(ctx):
+    """Model calls synchronise or allocate: each is refused while a recording
+    is open, leaves the model as it was, and works again once it is closed."""
+    cfg = cw.make_config(2, 256, 4, 2, 128, 512, 64, 16, cw.CW_F16, 1e-6, 1e6)
+    m = cw.Model(ctx, cfg)
+    m.load_synthetic(7)
+    m.finalize()
+    want = m.step(3, 0)
+    ctx.graph_begin()
+    for call in (lambda: m.step(3, 0), lambda: m.set_taps(True),
+                 lambda: m.decode_async(1, mode=cw.STEP_GRAPH), lambda: m.prefill([1, 2]),
+                 lambda: cw.Model(ctx, cfg)):
+        with pytest.raises(cw.CwError, match="while a graph is being recorded"):
+            call()
+    ctx.graph_end().close()
+    assert m.step(3, 0) == want
+    m.close()
