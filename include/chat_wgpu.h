@@ -88,7 +88,8 @@ int cw_flush(cw_ctx *ctx);
  * that would allocate or synchronise fail with CW_ERR_STATE (uploads,
  * downloads, flush, profiling, a first frame-arena chunk, kernel scratch or
  * RoPE table at a new size): run the sequence once before recording.  The
- * cw_model_* calls keep their own graph and are not recordable. */
+ * cw_model_* and cw_generate calls keep their own graph and are not
+ * recordable: while recording they return CW_ERR_STATE and change nothing. */
 int cw_graph_begin(cw_ctx *ctx);
 int cw_graph_end(cw_ctx *ctx, cw_graph **out);
 int cw_graph_launch(cw_ctx *ctx, const cw_graph *g);
