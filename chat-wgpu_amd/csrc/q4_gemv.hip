@@ -321,7 +321,8 @@ gemv_fn pick_xs(int xs, int epi) {
 }
 
 // PD: one group in flight per wave, two for single-row tiles of long rows
-// (steps per tile S >= 4), where it measured faster.
+// (steps per tile S >= 3), where it measured faster (3072 x 1024: 4.8-4.9
+// against 5.2 us; at S = 2, 4096 x 4096, one group is faster).
 template <int G>
 gemv_fn pick_r(int r, int xs, int epi, bool deep) {
     if (r == 2) return pick_xs<G, 2, 1>(xs, epi);
@@ -407,7 +408,7 @@ int launch_q4_gemv(cw_ctx *ctx, XSrc xs, Epi epi, const GemvArgs &a) {
                       ? 2
                       : 1;
     const int n_tiles = tiles_for(r);
-    gemv_fn fn = pick(g, r, xs, epi, nb / g >= 4);
+    gemv_fn fn = pick(g, r, xs, epi, nb / g >= 3);
     const int lds = nb * 132;
     int occ = 1;
     CW_TRY(occupancy(fn, lds, &occ));  // raises the kernel's LDS limit
