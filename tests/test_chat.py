@@ -154,3 +154,47 @@ def test_load_tokenizer_forms(tok, tmp_path):
     want = tok.encode(text).ids
     for src in (js, js.encode(), str(p), tok):
         assert chat.load_tokenizer(src).encode(text).ids == want
+
+
+class ScriptedDeviceLoop(ScriptedModel):
+    """A stand-in that also has the device decode loop: after prefill the
+    state is (next id, position) on the "device"; decode_async(1) feeds that
+    id at that position and appends the next id to the token record."""
+
+    def prefill(self, ids):
+        nxt = super().prefill(ids)
+        self.state = (nxt, len(ids))
+        self.record = []
+        return nxt
+
+    def decode_async(self, n_steps, mode):
+        assert mode == chat.STEP_GRAPH
+        for _ in range(n_steps):
+            token, pos = self.state
+            self.fed.append((int(token), int(pos)))
+            nxt = self._next()
+            self.record.append(nxt)
+            self.state = (nxt, pos + 1)
+
+    def tokens(self, n):
+        return self.record[:n]
+
+    def step(self, token, pos):  # never used after a batched prompt phase
+        raise AssertionError("eager step after the batched prompt phase")
+
+
+def test_graph_loop_after_batched_prompt(tok):
+    """After the batched prompt phase every reply token comes from one
+    replay of the device step, fed the previous id at the next position."""
+    a, b = tok.token_to_id("a"), tok.token_to_id("b")
+    eos = tok.token_to_id("<|im_end|>")
+    m = ScriptedDeviceLoop([a, b, a, eos, b])
+    lc = chat.LocalChat(m, tok)
+    text = lc.generate("x", max_tokens=8)
+    n = len(lc.last_prompt_ids)
+    assert lc.last_reply_ids == [a, b, a]
+    assert text == "aba"
+    assert m.fed == [(a, n), (b, n + 1), (a, n + 2)]
+    # the per-token prompt path keeps the eager steps
+    m2 = ScriptedModel([a] * len(lc.last_prompt_ids) + [b, eos])
+    assert chat.LocalChat(m2, tok).generate("x", max_tokens=8, batched_prefill=False) == "ab"
