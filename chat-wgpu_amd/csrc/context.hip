@@ -109,11 +109,14 @@ static int refuse_while_capturing(const cw_ctx *ctx, const char *what) {
 int ctx_scratch(cw_ctx *ctx, size_t bytes, void **out) {
     if (bytes > ctx->scratch_size) {
         CW_TRY(refuse_while_capturing(ctx, "kernel scratch must grow"));
-        CW_HIP(hipStreamSynchronize(ctx->stream));
-        if (ctx->scratch) CW_HIP(hipFree(ctx->scratch));
-        ctx->scratch = nullptr;
         size_t sz = bytes < (1u << 20) ? (1u << 20) : bytes;
-        CW_HIP(hipMalloc(&ctx->scratch, sz));
+        void *p = nullptr;
+        CW_HIP(hipMalloc(&p, sz));
+        // a launch sequence recorded earlier (cw_graph_*) still names the old
+        // buffer; replaying it must not write freed memory, so the old buffer
+        // is retired, not freed, until the context is destroyed
+        if (ctx->scratch) ctx->scratch_retired.push_back(ctx->scratch);
+        ctx->scratch = p;
         // counters inside scratch must start at zero (cleared in stream order)
         CW_HIP(hipMemsetAsync(ctx->scratch, 0, sz, ctx->stream));
         ctx->scratch_size = sz;
@@ -239,6 +242,7 @@ int cw_ctx_destroy(cw_ctx *ctx) {
     for (void *p : ctx->allocs) hipFree(p);
     for (auto &c : ctx->chunks) hipFree(c.base);
     if (ctx->scratch) hipFree(ctx->scratch);
+    for (void *p : ctx->scratch_retired) hipFree(p);
     if (ctx->attn_cnt) hipFree(ctx->attn_cnt);
     for (auto &t : ctx->ropes) {
         hipFree(t.cos_t);

@@ -7,6 +7,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdint>
+#include <deque>
 #include <string>
 #include <thread>
 #include <vector>
@@ -103,8 +104,12 @@ struct cw_ctx {
     // standalone kernel entry points; grows on demand between launches
     void *scratch = nullptr;
     size_t scratch_size = 0;
+    // smaller scratch buffers a larger request replaced: a recorded launch
+    // sequence may still name them, so they live until cw_ctx_destroy
+    std::vector<void *> scratch_retired;
 
-    std::vector<cw_rope_tab> ropes;
+    // RoPE tables; a deque, so a table's address stays valid as others are added
+    std::deque<cw_rope_tab> ropes;
 
     // a cw_graph_begin .. cw_graph_end recording is open on the stream
     bool capturing = false;
@@ -307,6 +312,19 @@ struct StepArgs {
     long long timeout;        // barrier spin limit in wall-clock ticks
     long long *trace;         // optional phase stamps (workgroup 0), else null
 };
+
+// A device allocation [p, p + bytes) the fused step may touch.
+struct Extent {
+    const void *p;
+    size_t bytes;
+};
+// Host-side check of the fused step's buffer layout: every range that any
+// phase of the step reads or writes (weights, activations, caches, partials,
+// counters), computed from the same phase table the kernel uses, must lie
+// inside one of `ext`.  `a.layers` must point at the host copy of the layer
+// table.  Returns false with the first offending range in *why.
+bool step_check_ranges(const StepArgs &a, int kv_dtype, int head_dim, int n_cu,
+                       const std::vector<Extent> &ext, std::string *why);
 
 size_t step_sync_words();
 int step_sync_err_index();

@@ -868,7 +868,9 @@ struct PhaseSpec {
     const float *resid;
 };
 
-__device__ __forceinline__ PhaseSpec phase_spec(const StepArgs &a, int l, int kind, uint32_t token) {
+// (host and device: the host-side range check walks the same table)
+__host__ __device__ inline PhaseSpec phase_spec(const StepArgs &a, int l, int kind, uint32_t token,
+                                              bool first_wg) {
     const int q_dim = a.n_heads * kHD, qkv_n = q_dim + 2 * a.n_kv * kHD;
     const float *h_in = l == 0 ? a.embed + (size_t)token * a.dim : a.h_a + (size_t)l * a.dim;
     PhaseSpec f{};
@@ -880,7 +882,7 @@ __device__ __forceinline__ PhaseSpec phase_spec(const StepArgs &a, int l, int ki
         f.xmode = X_NORM;
         f.src = a.h_a + (size_t)a.n_layers * a.dim;
         f.normw = a.final_norm;
-        f.copy_out = blockIdx.x == 0 ? a.hidden_out : nullptr;
+        f.copy_out = first_wg ? a.hidden_out : nullptr;
         f.epi = E_LOGITS;
         f.out = a.logits;
         return f;
@@ -930,6 +932,126 @@ __device__ __forceinline__ PhaseSpec phase_spec(const StepArgs &a, int l, int ki
     return f;
 }
 
+// ---------------------------------------------------------------- host-side range check
+
+struct RangeCheck {
+    const std::vector<cwi::Extent> &ext;
+    std::string *why;
+    bool ok = true;
+    // [p, p + bytes) must lie inside one extent
+    void need(const void *p, size_t bytes, const char *what, int layer) {
+        if (!ok) return;
+        const uintptr_t lo = reinterpret_cast<uintptr_t>(p), hi = lo + bytes;
+        for (const auto &e : ext) {
+            const uintptr_t b = reinterpret_cast<uintptr_t>(e.p);
+            if (lo >= b && hi <= b + e.bytes) return;
+        }
+        ok = false;
+        char buf[224];
+        size_t best = 0;
+        uintptr_t bb = 0;
+        for (const auto &e : ext) {  // the extent the range starts in, if any
+            const uintptr_t b = reinterpret_cast<uintptr_t>(e.p);
+            if (lo >= b && lo < b + e.bytes) {
+                bb = b;
+                best = e.bytes;
+            }
+        }
+        if (best)
+            snprintf(buf, sizeof buf,
+                     "layer %d %s reads/writes %zu bytes at offset %zu of a %zu-byte allocation "
+                     "(%zu bytes past its end)",
+                     layer, what, bytes, (size_t)(lo - bb), best, (size_t)(hi - (bb + best)));
+        else
+            snprintf(buf, sizeof buf, "layer %d %s: %zu bytes outside every allocation", layer,
+                     what, bytes);
+        *why = buf;
+    }
+};
+
+const char *kPhaseName[6] = {"QKV", "ATTN", "O", "GATE|UP", "DOWN", "LM head"};
+
+}  // namespace
+
+namespace cwi {
+
+bool step_check_ranges(const StepArgs &a, int kv_dtype, int head_dim, int n_cu,
+                       const std::vector<Extent> &ext, std::string *why) {
+    RangeCheck rc{ext, why};
+    const size_t es = kv_dtype == CW_F16 ? 2 : 4;
+    const size_t q_dim = (size_t)a.n_heads * head_dim, kv_dim = (size_t)a.n_kv * head_dim;
+    const size_t qkv_n = q_dim + 2 * kv_dim;
+    char what[64];
+    // GEMV phases: the phase table the kernel uses, for the first and the
+    // last token id (layer 0 reads the token's embedding row)
+    for (uint32_t token : {0u, (uint32_t)(a.vocab - 1)}) {
+        for (int l = 0; l <= a.n_layers; ++l) {
+            for (int kind = 0; kind < 5; ++kind) {
+                const bool lm = l == a.n_layers;
+                if (lm && kind != 0) break;
+                const int k = lm ? P_LM : kind;
+                if (k == P_ATTN) continue;
+                const PhaseSpec f = phase_spec(a, lm ? 0 : l, k, token, true);
+                const size_t nblk = (size_t)f.N * (f.K / 32);
+                snprintf(what, sizeof what, "%s quants", kPhaseName[k]);
+                rc.need(f.q, nblk * 16, what, l);
+                snprintf(what, sizeof what, "%s scales", kPhaseName[k]);
+                rc.need(f.sc, nblk * 2, what, l);
+                snprintf(what, sizeof what, "%s input", kPhaseName[k]);
+                rc.need(f.src, (size_t)f.K * 4 * (f.xmode == X_SWIGLU ? 2 : 1), what, l);
+                if (f.xmode == X_NORM) {
+                    snprintf(what, sizeof what, "%s norm gain", kPhaseName[k]);
+                    rc.need(f.normw, (size_t)f.K * 4, what, l);
+                }
+                if (f.copy_out) {
+                    snprintf(what, sizeof what, "%s normed copy", kPhaseName[k]);
+                    rc.need(f.copy_out, (size_t)f.K * 4, what, l);
+                }
+                snprintf(what, sizeof what, "%s output", kPhaseName[k]);
+                rc.need(f.out, (size_t)f.N * 4, what, l);
+                if (f.epi == E_RESID) {
+                    snprintf(what, sizeof what, "%s residual", kPhaseName[k]);
+                    rc.need(f.resid, (size_t)f.N * 4, what, l);
+                }
+            }
+        }
+    }
+    // attention phases: raw q|k|v row, QK-norm gains, RoPE rows of every
+    // position, the whole cache of the layer, the chunk partials, the output
+    const size_t half = (size_t)head_dim / 2;
+    for (int l = 0; l < a.n_layers; ++l) {
+        const StepLayer &L = a.layers[l];
+        rc.need(a.qkv + (size_t)l * qkv_n, qkv_n * 4, "ATTN q|k|v", l);
+        rc.need(L.q_norm, (size_t)head_dim * 4, "ATTN q norm gain", l);
+        rc.need(L.k_norm, (size_t)head_dim * 4, "ATTN k norm gain", l);
+        rc.need(a.cos_t, (size_t)a.max_seq * half * 4, "ATTN RoPE cos", l);
+        rc.need(a.sin_t, (size_t)a.max_seq * half * 4, "ATTN RoPE sin", l);
+        rc.need(L.kc, (size_t)a.max_seq * kv_dim * es, "ATTN K cache", l);
+        rc.need(L.vc, (size_t)a.max_seq * kv_dim * es, "ATTN V cache", l);
+        rc.need(a.part, (size_t)a.n_heads * a.max_chunks * (head_dim + 2) * 4, "ATTN partials", l);
+        rc.need(a.attn + (size_t)l * q_dim, q_dim * 4, "ATTN output", l);
+    }
+    // at most (max_seq + 7) / 8 chunks (8-position minimum) fit the partials
+    if (rc.ok && (a.max_seq + 7) / 8 > a.max_chunks) {
+        rc.ok = false;
+        *why = "attention partials hold fewer chunks than the cache can need";
+    }
+    // the argmax merge, the counters and the decode state
+    rc.need(a.am_v, (size_t)n_cu * 4, "LM head argmax values", a.n_layers);
+    rc.need(a.am_i, (size_t)n_cu * 4, "LM head argmax ids", a.n_layers);
+    rc.need(a.sync, step_sync_words() * 4, "grid counters", a.n_layers);
+    rc.need(a.hidden_out, (size_t)a.dim * 4, "final hidden state", a.n_layers);
+    rc.need(a.state, sizeof(GenState), "decode state", a.n_layers);
+    rc.need(a.prompt, (size_t)a.max_seq * 4, "prompt ids", a.n_layers);
+    rc.need(a.tokens, (size_t)a.max_seq * 4, "produced ids", a.n_layers);
+    rc.need(a.argmax_out, 4, "argmax output", a.n_layers);
+    return rc.ok;
+}
+
+}  // namespace cwi
+
+namespace {
+
 // The step is a loop over its phase list, so each kind of work exists once in
 // the code: the loop body stays small enough for the instruction cache.
 template <typename KVT, int HPK>
@@ -970,7 +1092,7 @@ __global__ __launch_bounds__(kT) void decode_step_kernel(const StepArgs *__restr
     {
         const StepArgs &a = *fresh(ap);
         geo = attn_geo<KVT, HPK>(a, pos);
-        const PhaseSpec f = phase_spec(a, 0, P_QKV, token);
+        const PhaseSpec f = phase_spec(a, 0, P_QKV, token, blockIdx.x == 0);
         p = gemv_setup(f.q, f.sc, f.N, f.K, gw, nw);
         gemv_prefetch(p, rq, rd);
     }
@@ -987,7 +1109,7 @@ __global__ __launch_bounds__(kT) void decode_step_kernel(const StepArgs *__restr
             if (kind == P_ATTN) {  // QK-norm, RoPE, KV write, attention (qwen3.rs:154-177)
                 attn_phase<KVT, HPK>(a, a.layers[l], l, geo, rq, lds, merge_s);
             } else {
-                const PhaseSpec f = phase_spec(a, l, kind, token);
+                const PhaseSpec f = phase_spec(a, l, kind, token, blockIdx.x == 0);
                 stage_x(f.xmode, f.src, f.normw, f.K, a.eps, lds4, sx, red, f.copy_out,
                         [&] { gemv_fill(p, rq, rd); });
                 mark(a, ph, 0);
@@ -1006,7 +1128,7 @@ __global__ __launch_bounds__(kT) void decode_step_kernel(const StepArgs *__restr
             if (nk == P_ATTN) {
                 attn_prefetch<KVT, HPK>(a, a.layers[nl], geo, rq);
             } else {
-                const PhaseSpec f = phase_spec(a, nl, nk, token);
+                const PhaseSpec f = phase_spec(a, nl, nk, token, blockIdx.x == 0);
                 p = gemv_setup(f.q, f.sc, f.N, f.K, gw, nw);
                 gemv_prefetch(p, rq, rd);
             }

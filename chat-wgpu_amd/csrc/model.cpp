@@ -35,8 +35,9 @@ struct Q4W {
 
 struct Layer {
     float *attn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *ffn_norm = nullptr;
-    // q|k|v rows in one matrix
-    Q4W qkv, wo, gate, up, down;
+    // q|k|v rows in one matrix; gate then up rows in one matrix `gu`
+    // [2*hidden][dim], with `gate` and `up` its two halves
+    Q4W qkv, wo, gu, gate, up, down;
 };
 
 // tensor ids within a layer
@@ -71,6 +72,16 @@ struct cw_model {
     GenState *state = nullptr;
     uint32_t *prompt_dev = nullptr, *tokens_dev = nullptr, *argmax_out = nullptr;
     bool finalized = false;
+    // every device allocation of the model, for the fused step's range check
+    std::vector<Extent> extents;
+    // dry plan: addresses are handed out from an unmapped range and nothing
+    // touches a device (cw_step_layout_check); `dry_split_gu` lays gate and up
+    // out as two allocations, the layout the step's range check refuses
+    bool dry = false;
+    bool dry_split_gu = false;
+    int dry_n_cu = 0;
+    uintptr_t dry_next = 0;
+    char fused_why[256] = {0};
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
     std::vector<void *> allocs;
@@ -110,8 +121,17 @@ int refuse_recording(const cw_model *m, const char *what) {
 
 int dalloc(cw_model *m, size_t bytes, void **out) {
     void *p = nullptr;
-    CW_HIP(hipMalloc(&p, bytes));
-    m->allocs.push_back(p);
+    if (m->dry) {
+        // page-aligned, one unmapped page between allocations, so a range
+        // that runs past its buffer never lands inside the next one
+        m->dry_next = (m->dry_next + 4095) & ~(uintptr_t)4095;
+        p = reinterpret_cast<void *>(m->dry_next);
+        m->dry_next += bytes + 4096;
+    } else {
+        CW_HIP(hipMalloc(&p, bytes));
+        m->allocs.push_back(p);
+    }
+    m->extents.push_back(Extent{p, bytes});
     *out = p;
     return CW_OK;
 }
@@ -123,6 +143,17 @@ int alloc_q4(cw_model *m, Q4W &w, int out_f, int in_f) {
     CW_TRY(dalloc(m, nblk * 2, (void **)&w.s));
     CW_TRY(dalloc(m, nblk * 16, (void **)&w.q));
     return CW_OK;
+}
+
+// rows [row0, row0 + rows) of w as a matrix of its own (no allocation)
+Q4W q4_rows(const Q4W &w, int row0, int rows) {
+    const size_t nb = w.in_f / 32;
+    Q4W v;
+    v.s = w.s + (size_t)row0 * nb;
+    v.q = w.q + (size_t)row0 * nb * 16;
+    v.out_f = rows;
+    v.in_f = w.in_f;
+    return v;
 }
 
 int upload_rows(cw_model *m, Q4W &w, int row0, int rows, const uint16_t *s, const uint8_t *q) {
@@ -327,14 +358,12 @@ int run_steps(cw_model *m, int n, int mode) {
     return CW_OK;
 }
 
-// Buffers and the layer table of the fused step (after every weight exists).
-int setup_fused(cw_model *m) {
+// The fused step's layer table (host copy) and argument block, with the
+// buffers it owns; nothing is uploaded or launched (so the dry plan runs it).
+int build_step(cw_model *m, std::vector<StepLayer> &host) {
     const auto &c = m->cfg;
-    m->fused_unsupported = step_unsupported(c.head_dim, c.n_heads / c.n_kv_heads, c.n_kv_heads,
-                                            c.dim, m->q_dim, c.hidden, c.max_seq);
-    if (m->fused_unsupported) return CW_OK;
     const int L = c.n_layers;
-    std::vector<StepLayer> host(L);
+    host.assign(L, StepLayer{});
     for (int i = 0; i < L; ++i) {
         const Layer &y = m->layers[i];
         StepLayer &s = host[i];
@@ -346,10 +375,12 @@ int setup_fused(cw_model *m) {
         s.qkv_s = y.qkv.s;
         s.o_q = y.wo.q;
         s.o_s = y.wo.s;
-        // the fused step reads gate|up as one [2*hidden][dim] matrix; the
-        // separate allocations below are not that layout (the step is off)
-        s.gu_q = y.gate.q;
-        s.gu_s = y.gate.s;
+        // the step reads gate|up as one [2*hidden][dim] matrix: `gu`, of
+        // which gate and up are the halves (a split plan hands it the gate
+        // matrix alone, the layout the range check below refuses)
+        const Q4W &gu = m->dry_split_gu ? y.gate : y.gu;
+        s.gu_q = gu.q;
+        s.gu_s = gu.s;
         s.down_q = y.down.q;
         s.down_s = y.down.s;
         s.kc = (char *)m->kcache + (size_t)i * m->kv_layer_bytes;
@@ -357,21 +388,17 @@ int setup_fused(cw_model *m) {
     }
     StepArgs &a = m->step;
     CW_TRY(dalloc(m, sizeof(StepLayer) * L, (void **)&m->step_layers));
-    CW_TRY(cw_upload(m->ctx, m->step_layers, host.data(), sizeof(StepLayer) * L));
     const int max_chunks = (c.max_seq + 7) / 8;
+    const int n_cu = m->dry ? m->dry_n_cu : m->ctx->n_cu;
     CW_TRY(dalloc(m, (size_t)(L + 1) * c.dim * 4, (void **)&a.h_a));
     CW_TRY(dalloc(m, (size_t)L * c.dim * 4, (void **)&a.h_b));
     CW_TRY(dalloc(m, (size_t)L * (m->q_dim + 2 * m->kv_dim) * 4, (void **)&a.qkv));
     CW_TRY(dalloc(m, (size_t)L * m->q_dim * 4, (void **)&a.attn));
     CW_TRY(dalloc(m, (size_t)L * 2 * c.hidden * 4, (void **)&a.act));
     CW_TRY(dalloc(m, (size_t)c.n_heads * max_chunks * (c.head_dim + 2) * 4, (void **)&a.part));
-    CW_TRY(dalloc(m, (size_t)m->ctx->n_cu * 4, (void **)&a.am_v));
-    CW_TRY(dalloc(m, (size_t)m->ctx->n_cu * 4, (void **)&a.am_i));
+    CW_TRY(dalloc(m, (size_t)n_cu * 4, (void **)&a.am_v));
+    CW_TRY(dalloc(m, (size_t)n_cu * 4, (void **)&a.am_i));
     CW_TRY(dalloc(m, step_sync_words() * 4, (void **)&m->step_sync));
-    CW_HIP(hipMemsetAsync(m->step_sync, 0, step_sync_words() * 4, m->ctx->stream));
-    int rate_khz = 0;
-    CW_HIP(hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, m->ctx->device));
-    if (rate_khz <= 0) rate_khz = 100000;
     a.layers = m->step_layers;
     a.n_layers = L;
     a.dim = c.dim;
@@ -396,10 +423,44 @@ int setup_fused(cw_model *m) {
     a.prompt = m->prompt_dev;
     a.tokens = m->tokens_dev;
     a.argmax_out = m->argmax_out;
-    a.timeout = (long long)rate_khz * 1000 * 2;  // 2 s
     a.trace = nullptr;
     CW_TRY(dalloc(m, sizeof(StepArgs), (void **)&m->step_dev));
-    CW_TRY(cw_upload(m->ctx, m->step_dev, &a, sizeof(StepArgs)));
+    return CW_OK;
+}
+
+// The step's range check over the model's allocations: false (with the
+// reason in m->fused_why) when some phase would touch memory outside them.
+bool check_step(cw_model *m, const std::vector<StepLayer> &host) {
+    StepArgs a = m->step;
+    a.layers = host.data();
+    std::string why;
+    const int n_cu = m->dry ? m->dry_n_cu : m->ctx->n_cu;
+    if (step_check_ranges(a, m->cfg.kv_dtype, m->cfg.head_dim, n_cu, m->extents, &why))
+        return true;
+    snprintf(m->fused_why, sizeof m->fused_why, "buffer layout check failed: %s", why.c_str());
+    return false;
+}
+
+// Buffers and the layer table of the fused step (after every weight exists).
+int setup_fused(cw_model *m) {
+    const auto &c = m->cfg;
+    m->fused_unsupported = step_unsupported(c.head_dim, c.n_heads / c.n_kv_heads, c.n_kv_heads,
+                                            c.dim, m->q_dim, c.hidden, c.max_seq);
+    if (m->fused_unsupported) return CW_OK;
+    std::vector<StepLayer> host;
+    CW_TRY(build_step(m, host));
+    if (!check_step(m, host)) {
+        m->fused_unsupported = m->fused_why;
+        return CW_OK;
+    }
+    if (m->dry) return CW_OK;
+    CW_TRY(cw_upload(m->ctx, m->step_layers, host.data(), sizeof(StepLayer) * host.size()));
+    CW_HIP(hipMemsetAsync(m->step_sync, 0, step_sync_words() * 4, m->ctx->stream));
+    int rate_khz = 0;
+    CW_HIP(hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, m->ctx->device));
+    if (rate_khz <= 0) rate_khz = 100000;
+    m->step.timeout = (long long)rate_khz * 1000 * 2;  // 2 s
+    CW_TRY(cw_upload(m->ctx, m->step_dev, &m->step, sizeof(StepArgs)));
     return CW_OK;
 }
 
@@ -519,6 +580,101 @@ int require_final(cw_model *m, const char *what) {
     return CW_OK;
 }
 
+// The configuration checks of cw_model_create.
+int check_config(const cw_model_config &cfg, const char *what) {
+    const auto &c = cfg;
+    CW_CHECK_ARG(c.family.norm_unit_gain == 0 && c.family.act == 0 && c.family.qk_norm == 1 &&
+                     c.family.qkv_bias == 0,
+                 "%s: only the qwen3 family spec is built (plain norm, SwiGLU, "
+                 "qk_norm, no qkv bias)", what);
+    CW_CHECK_ARG(c.n_layers > 0 && c.dim > 0 && c.n_heads > 0 && c.n_kv_heads > 0 &&
+                     c.hidden > 0 && c.vocab > 0 && c.max_seq > 0,
+                 "%s: every dimension must be positive", what);
+    CW_CHECK_ARG(c.max_seq <= 32768, "%s: max_seq=%d exceeds 32768", what, c.max_seq);
+    CW_CHECK_ARG(c.n_heads % c.n_kv_heads == 0, "%s: n_heads %% n_kv_heads != 0", what);
+    const int hpk = c.n_heads / c.n_kv_heads;
+    CW_CHECK_ARG(hpk == 1 || hpk == 2 || hpk == 4 || hpk == 8,
+                 "%s: heads per kv head %d not in {1,2,4,8}", what, hpk);
+    CW_CHECK_ARG(c.head_dim == 16 || c.head_dim == 32 || c.head_dim == 64 || c.head_dim == 128 ||
+                     c.head_dim == 256,
+                 "%s: head_dim=%d not in {16,32,64,128,256}", what, c.head_dim);
+    const int q_dim = c.n_heads * c.head_dim;
+    CW_CHECK_ARG(c.dim % 32 == 0 && c.hidden % 32 == 0 && q_dim % 32 == 0,
+                 "%s: dim, hidden and n_heads*head_dim must be multiples of 32", what);
+    CW_CHECK_ARG(c.dim <= 32768 && c.hidden <= 32768 && q_dim <= 32768,
+                 "%s: GEMV input width above 32768", what);
+    CW_CHECK_ARG(c.kv_dtype == CW_F32 || c.kv_dtype == CW_F16, "%s: kv_dtype=%d", what,
+                 c.kv_dtype);
+    return CW_OK;
+}
+
+// Every device buffer of the model (weights, cache, activations, decode
+// state) for config c, in a fixed order; in a dry plan nothing touches a
+// device.
+int model_alloc(cw_model *m, const cw_model_config &c) {
+    const int q_dim = c.n_heads * c.head_dim, kv_dim = c.n_kv_heads * c.head_dim;
+    m->cfg = c;
+    m->q_dim = q_dim;
+    m->kv_dim = kv_dim;
+    m->layers.resize(c.n_layers);
+    m->have.assign(c.n_layers, std::vector<bool>(T_N, false));
+    for (auto &L : m->layers) {
+        CW_TRY(dalloc(m, c.dim * 4, (void **)&L.attn_norm));
+        CW_TRY(dalloc(m, c.head_dim * 4, (void **)&L.q_norm));
+        CW_TRY(dalloc(m, c.head_dim * 4, (void **)&L.k_norm));
+        CW_TRY(dalloc(m, c.dim * 4, (void **)&L.ffn_norm));
+        CW_TRY(alloc_q4(m, L.qkv, q_dim + 2 * kv_dim, c.dim));
+        CW_TRY(alloc_q4(m, L.wo, c.dim, q_dim));
+        if (m->dry_split_gu) {
+            CW_TRY(alloc_q4(m, L.gate, c.hidden, c.dim));
+            CW_TRY(alloc_q4(m, L.up, c.hidden, c.dim));
+        } else {
+            CW_TRY(alloc_q4(m, L.gu, 2 * c.hidden, c.dim));
+            L.gate = q4_rows(L.gu, 0, c.hidden);
+            L.up = q4_rows(L.gu, c.hidden, c.hidden);
+        }
+        CW_TRY(alloc_q4(m, L.down, c.dim, c.hidden));
+    }
+    const size_t es = c.kv_dtype == CW_F16 ? 2 : 4;
+    m->kv_layer_bytes = (size_t)c.max_seq * kv_dim * es;
+    const size_t part_floats = attn_scratch_floats(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq);
+    CW_TRY(dalloc(m, (size_t)c.vocab * c.dim * 4, (void **)&m->embed));
+    CW_TRY(dalloc(m, c.dim * 4, (void **)&m->final_norm));
+    CW_TRY(alloc_q4(m, m->lm_head, c.vocab, c.dim));
+    CW_TRY(dalloc(m, m->kv_layer_bytes * c.n_layers, &m->kcache));
+    CW_TRY(dalloc(m, m->kv_layer_bytes * c.n_layers, &m->vcache));
+    CW_TRY(dalloc(m, c.dim * 4, (void **)&m->hidden));
+    CW_TRY(dalloc(m, c.dim * 4, (void **)&m->hidden_out));
+    CW_TRY(dalloc(m, (size_t)(q_dim + 2 * kv_dim) * 4, (void **)&m->qkv));
+    CW_TRY(dalloc(m, (size_t)q_dim * 4, (void **)&m->attn));
+    CW_TRY(dalloc(m, (size_t)c.hidden * 4, (void **)&m->act));
+    CW_TRY(dalloc(m, (size_t)c.vocab * 4, (void **)&m->logits));
+    CW_TRY(dalloc(m, part_floats * 4, (void **)&m->part));
+    CW_TRY(dalloc(m, argmax_scratch_bytes(c.vocab), &m->argmax_scratch));
+    CW_TRY(dalloc(m, sizeof(GenState), (void **)&m->state));
+    CW_TRY(dalloc(m, (size_t)c.max_seq * 4, (void **)&m->prompt_dev));
+    CW_TRY(dalloc(m, (size_t)c.max_seq * 4, (void **)&m->tokens_dev));
+    CW_TRY(dalloc(m, 4, (void **)&m->argmax_out));
+    // the RoPE table [max_pos][hd/2] (shared through the context); in a dry
+    // plan, a table of the context's size for this max_seq
+    int max_pos = 1024;
+    while (max_pos < c.max_seq) max_pos *= 2;
+    const size_t tab = (size_t)max_pos * (c.head_dim / 2) * 4;
+    if (m->dry) {
+        CW_TRY(dalloc(m, tab, (void **)&m->cos_t));
+        CW_TRY(dalloc(m, tab, (void **)&m->sin_t));
+    } else {
+        const cw_rope_tab *t = nullptr;
+        CW_TRY(ctx_rope_table(m->ctx, c.rope_theta, c.head_dim, c.max_seq, &t));
+        m->cos_t = t->cos_t;
+        m->sin_t = t->sin_t;
+        const size_t n = (size_t)t->max_pos * (c.head_dim / 2) * 4;
+        m->extents.push_back(Extent{t->cos_t, n});
+        m->extents.push_back(Extent{t->sin_t, n});
+    }
+    return CW_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -531,85 +687,47 @@ int cw_model_create(cw_ctx *ctx, const cw_model_config *cfg, cw_model **out) {
                   "cw_graph_end)");
         return CW_ERR_STATE;
     }
+    CW_TRY(check_config(*cfg, "cw_model_create"));
     const auto &c = *cfg;
-    CW_CHECK_ARG(c.family.norm_unit_gain == 0 && c.family.act == 0 && c.family.qk_norm == 1 &&
-                     c.family.qkv_bias == 0,
-                 "cw_model_create: only the qwen3 family spec is built (plain norm, SwiGLU, "
-                 "qk_norm, no qkv bias)");
-    CW_CHECK_ARG(c.n_layers > 0 && c.dim > 0 && c.n_heads > 0 && c.n_kv_heads > 0 &&
-                     c.hidden > 0 && c.vocab > 0 && c.max_seq > 0,
-                 "cw_model_create: every dimension must be positive");
-    CW_CHECK_ARG(c.max_seq <= 32768, "cw_model_create: max_seq=%d exceeds 32768", c.max_seq);
-    CW_CHECK_ARG(c.n_heads % c.n_kv_heads == 0, "cw_model_create: n_heads %% n_kv_heads != 0");
-    const int hpk = c.n_heads / c.n_kv_heads;
-    CW_CHECK_ARG(hpk == 1 || hpk == 2 || hpk == 4 || hpk == 8,
-                 "cw_model_create: heads per kv head %d not in {1,2,4,8}", hpk);
-    CW_CHECK_ARG(c.head_dim == 16 || c.head_dim == 32 || c.head_dim == 64 || c.head_dim == 128 ||
-                     c.head_dim == 256,
-                 "cw_model_create: head_dim=%d not in {16,32,64,128,256}", c.head_dim);
-    const int q_dim = c.n_heads * c.head_dim, kv_dim = c.n_kv_heads * c.head_dim;
-    CW_CHECK_ARG(c.dim % 32 == 0 && c.hidden % 32 == 0 && q_dim % 32 == 0,
-                 "cw_model_create: dim, hidden and n_heads*head_dim must be multiples of 32");
-    CW_CHECK_ARG(c.dim <= 32768 && c.hidden <= 32768 && q_dim <= 32768,
-                 "cw_model_create: GEMV input width above 32768");
-    CW_CHECK_ARG(c.kv_dtype == CW_F32 || c.kv_dtype == CW_F16, "cw_model_create: kv_dtype=%d",
-                 c.kv_dtype);
-
     cw_model *m = new cw_model();
     m->ctx = ctx;
-    m->cfg = c;
-    m->q_dim = q_dim;
-    m->kv_dim = kv_dim;
-    m->layers.resize(c.n_layers);
-    m->have.assign(c.n_layers, std::vector<bool>(T_N, false));
-    auto fail = [&](int rc) {
+    int rc = model_alloc(m, c);
+    if (rc != CW_OK) {
         cw_model_destroy(m);
         return rc;
-    };
-    int rc;
-    for (auto &L : m->layers) {
-        if ((rc = dalloc(m, c.dim * 4, (void **)&L.attn_norm)) ||
-            (rc = dalloc(m, c.head_dim * 4, (void **)&L.q_norm)) ||
-            (rc = dalloc(m, c.head_dim * 4, (void **)&L.k_norm)) ||
-            (rc = dalloc(m, c.dim * 4, (void **)&L.ffn_norm)) ||
-            (rc = alloc_q4(m, L.qkv, q_dim + 2 * kv_dim, c.dim)) ||
-            (rc = alloc_q4(m, L.wo, c.dim, q_dim)) || (rc = alloc_q4(m, L.gate, c.hidden, c.dim)) ||
-            (rc = alloc_q4(m, L.up, c.hidden, c.dim)) || (rc = alloc_q4(m, L.down, c.dim, c.hidden)))
-            return fail(rc);
     }
-    const size_t es = c.kv_dtype == CW_F16 ? 2 : 4;
-    m->kv_layer_bytes = (size_t)c.max_seq * kv_dim * es;
-    const size_t part_floats = attn_scratch_floats(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq);
-    if ((rc = dalloc(m, (size_t)c.vocab * c.dim * 4, (void **)&m->embed)) ||
-        (rc = dalloc(m, c.dim * 4, (void **)&m->final_norm)) ||
-        (rc = alloc_q4(m, m->lm_head, c.vocab, c.dim)) ||
-        (rc = dalloc(m, m->kv_layer_bytes * c.n_layers, &m->kcache)) ||
-        (rc = dalloc(m, m->kv_layer_bytes * c.n_layers, &m->vcache)) ||
-        (rc = dalloc(m, c.dim * 4, (void **)&m->hidden)) ||
-        (rc = dalloc(m, c.dim * 4, (void **)&m->hidden_out)) ||
-        (rc = dalloc(m, (size_t)(q_dim + 2 * kv_dim) * 4, (void **)&m->qkv)) ||
-        (rc = dalloc(m, (size_t)q_dim * 4, (void **)&m->attn)) ||
-        (rc = dalloc(m, (size_t)c.hidden * 4, (void **)&m->act)) ||
-        (rc = dalloc(m, (size_t)c.vocab * 4, (void **)&m->logits)) ||
-        (rc = dalloc(m, part_floats * 4, (void **)&m->part)) ||
-        (rc = dalloc(m, argmax_scratch_bytes(c.vocab), &m->argmax_scratch)) ||
-        (rc = dalloc(m, sizeof(GenState), (void **)&m->state)) ||
-        (rc = dalloc(m, (size_t)c.max_seq * 4, (void **)&m->prompt_dev)) ||
-        (rc = dalloc(m, (size_t)c.max_seq * 4, (void **)&m->tokens_dev)) ||
-        (rc = dalloc(m, 4, (void **)&m->argmax_out)))
-        return fail(rc);
     // zero the caches so positions never written read as 0, not garbage
     // cleared on the context stream, so every later copy and launch is ordered after
     if (hipMemsetAsync(m->kcache, 0, m->kv_layer_bytes * c.n_layers, ctx->stream) != hipSuccess ||
         hipMemsetAsync(m->vcache, 0, m->kv_layer_bytes * c.n_layers, ctx->stream) != hipSuccess) {
         set_error("cw_model_create: clearing the KV cache failed");
-        return fail(CW_ERR_HIP);
+        cw_model_destroy(m);
+        return CW_ERR_HIP;
     }
-    const cw_rope_tab *t = nullptr;
-    if ((rc = ctx_rope_table(ctx, c.rope_theta, c.head_dim, c.max_seq, &t))) return fail(rc);
-    m->cos_t = t->cos_t;
-    m->sin_t = t->sin_t;
     *out = m;
+    return CW_OK;
+}
+
+int cw_step_layout_check(const cw_model_config *cfg, int n_cu, int split_gate_up, char *why,
+                         size_t why_len) {
+    CW_CHECK_ARG(cfg && n_cu > 0, "cw_step_layout_check: bad argument");
+    CW_TRY(check_config(*cfg, "cw_step_layout_check"));
+    cw_model m;
+    m.dry = true;
+    m.dry_split_gu = split_gate_up != 0;
+    m.dry_n_cu = n_cu;
+    m.dry_next = (uintptr_t)1 << 44;
+    CW_TRY(model_alloc(&m, *cfg));
+    CW_TRY(setup_fused(&m));
+    const char *msg = m.fused_unsupported ? m.fused_unsupported : "";
+    if (why && why_len) snprintf(why, why_len, "%s", msg);
+    if (m.fused_unsupported == m.fused_why) {
+        set_error("cw_step_layout_check: %s", m.fused_why);
+        return CW_ERR_STATE;
+    }
+    CW_CHECK_ARG(m.fused_unsupported == nullptr,
+                 "cw_step_layout_check: the fused step does not cover this config: %s",
+                 m.fused_unsupported);
     return CW_OK;
 }
 

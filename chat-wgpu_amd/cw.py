@@ -17,6 +17,15 @@ LIB_PATH = os.path.join(_PKG, "libchatwgpu.so")
 CW_F32 = 0
 CW_F16 = 1
 
+# status codes (include/chat_wgpu.h)
+CW_OK = 0
+CW_ERR_ARG = -1
+CW_ERR_HIP = -2
+CW_ERR_OOM = -3
+CW_ERR_STATE = -4
+CW_ERR_FORMAT = -5
+CW_ERR_IO = -6
+
 STEP_EAGER = 0   # one launch per op
 STEP_GRAPH = 1   # the op launches of one step replayed as a HIP graph
 STEP_FUSED = 2   # one persistent cooperative kernel per step
@@ -104,6 +113,7 @@ _SIGS = {
     "cw_model_prefill": (_I, [_P, _P, _I, _I, C.POINTER(_U32)]),
     "cw_model_tokens": (_I, [_P, _P, _I, C.POINTER(_I)]),
     "cw_model_profile_step": (_I, [_P, _P, _I, C.POINTER(_I), C.POINTER(C.c_double)]),
+    "cw_step_layout_check": (_I, [C.POINTER(ModelConfig), _I, _I, C.c_char_p, _SZ]),
     "cw_gguf_open": (_I, [C.c_char_p, C.POINTER(_P)]),
     "cw_gguf_parse": (_I, [_P, _SZ, C.POINTER(_P)]),
     "cw_gguf_close": (_I, [_P]),
@@ -154,6 +164,15 @@ def _ptr(a):
 
 
 # ---------------------------------------------------------------- host-side helpers
+
+def step_layout_check(cfg, n_cu, split_gate_up=False):
+    """Host-only check of the fused decode step's buffer layout for cfg
+    (cw_step_layout_check): (rc, message); rc 0 when every range the step
+    touches lies inside an allocation."""
+    buf = C.create_string_buffer(256)
+    rc = lib().cw_step_layout_check(C.byref(cfg), int(n_cu), int(bool(split_gate_up)), buf, 256)
+    return rc, buf.value.decode()
+
 
 def q4_quantize(data):
     """Re-quantize f32 [out, in] to split GGUF Q4_0 (scales u16 [out, in/32], quants

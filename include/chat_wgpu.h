@@ -269,6 +269,20 @@ int cw_model_decode_async(cw_model *m, int n_steps, int mode);
  * [10L+4] per phase (5 per layer, then the LM head) two stamps: after
  * staging, after compute (20L+8 stamps in all); *tick_hz is the clock rate. */
 int cw_model_profile_step(cw_model *m, int64_t *ticks, int max_n, int *n_out, double *tick_hz);
+/* No counterpart in the reference: a host-only check, for tests and for
+ * callers that plan memory before creating a model, of the buffer layout the
+ * CW_STEP_FUSED kernel would use for cfg on a device of n_cu compute units.
+ * It lays out every buffer cw_model_create and the fused step allocate, at
+ * addresses that are never mapped (no device is touched), then walks the
+ * step's own phase table and checks that every range each phase reads or
+ * writes lies inside one allocation.  split_gate_up = 1 lays the gate and up
+ * projections out as two allocations while the step reads them as one
+ * [2*hidden][dim] matrix (a layout the check must refuse); 0 is the layout
+ * cw_model_create uses.  CW_OK when the layout holds; CW_ERR_STATE with the
+ * first offending range in why (and cw_last_error) when it does not;
+ * CW_ERR_ARG for configs the fused step does not cover. */
+int cw_step_layout_check(const cw_model_config *cfg, int n_cu, int split_gate_up, char *why,
+                         size_t why_len);
 /* Reset the decode state to (token, pos) without touching the cache. */
 /* The prompt phase of model::generate (src/model/mod.rs:57-125: P forwards,
  * the logits of all but the last discarded) for n tokens at positions

@@ -699,6 +699,23 @@ OR_API void or_model_prefill_kv(or_model *m, const void *k, const void *v, int n
     }
 }
 
+/* Read row `pos` of layer `layer`'s K and V caches back as f32 (f16 caches
+ * widened exactly), kv_dim values each: lets tests see which rows a step
+ * wrote (cache.rs:21-24 writes exactly one row per forward). */
+OR_API void or_model_kv_row(const or_model *m, int layer, int pos, float *k_out, float *v_out) {
+    size_t kv_dim = (size_t)m->n_kv * m->head_dim;
+    size_t off = ((size_t)layer * m->max_seq + pos) * kv_dim;
+    for (size_t j = 0; j < kv_dim; ++j) {
+        if (m->kv_f16) {
+            k_out[j] = or_f16_to_f32(((const uint16_t *)m->kcache)[off + j]);
+            v_out[j] = or_f16_to_f32(((const uint16_t *)m->vcache)[off + j]);
+        } else {
+            k_out[j] = ((const float *)m->kcache)[off + j];
+            v_out[j] = ((const float *)m->vcache)[off + j];
+        }
+    }
+}
+
 static void gemv(const or_q4 *w, const float *x, int in_f, int out_f, float *y) {
     or_q4_gemv(x, w->d, w->qs, in_f, out_f, y);
 }

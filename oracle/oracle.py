@@ -53,6 +53,7 @@ _SIGS = {
     "or_model_step": (None, [_P, C.c_uint32, _I, _P, _P, _P]),
     "or_model_step_taps": (None, [_P, C.c_uint32, _I, _P, _P, _P, _P, _P]),
     "or_generate": (_I, [_P, _P, _I, _I, _I, _P, _P]),
+    "or_model_kv_row": (None, [_P, _I, _I, _P, _P]),
     "or_set_threads": (None, [_I]),
     "or_get_threads": (_I, []),
 }
@@ -448,6 +449,14 @@ class OracleModel:
         k = np.ascontiguousarray(k)
         v = np.ascontiguousarray(v)
         lib().or_model_prefill_kv(self.h, _p(k), _p(v), n_pos)
+
+    def kv_row(self, layer, pos):
+        """Row `pos` of layer `layer`'s K and V caches as f32 arrays [kv_dim]."""
+        kvd = self.cfg.n_kv_heads * self.cfg.head_dim
+        k = np.empty(kvd, np.float32)
+        v = np.empty(kvd, np.float32)
+        lib().or_model_kv_row(self.h, int(layer), int(pos), _p(k), _p(v))
+        return k, v
 
     def step(self, token, pos, want_layers=False):
         logits = np.empty(self.cfg.vocab, np.float32)

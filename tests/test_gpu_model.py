@@ -160,6 +160,43 @@ def test_qwen3_8b_decode_prefilled(ctx):
     o.close()
 
 
+def test_qwen3_8b_teacher_forced_over_the_decode_range(ctx):
+    """Qwen3-8B shape (the decode workload's model) with a cache of 4352
+    positions of N(0,1) f16: one forward at each of 16 positions spread over
+    4096..4351 (attention over 4097..4352 keys), fed 16 different token ids
+    rather than the synthetic model's own greedy output (which repeats one
+    id).  Logits within 1e-3 of the oracle at every position and the same
+    argmax; the oracle's top-2 margins are printed."""
+    n_pre = 4352
+    cfg = qwen3_8b(n_pre)
+    weights = cw.synthetic_weights(cfg, 8009)
+    kv_n = cfg.n_layers * n_pre * cfg.n_kv_heads * cfg.head_dim
+    k = cw.synth_normal_f16(cw.synth_key(8009, "kv.k"), kv_n)
+    v = cw.synth_normal_f16(cw.synth_key(8009, "kv.v"), kv_n)
+    m, o = build_pair(ctx, cfg, weights)
+    m.prefill_kv(k, v, n_pre)
+    o.prefill_kv(k, v, n_pre)
+    del k, v
+    orc.set_threads(16)
+    positions = np.linspace(4096, 4351, 16).round().astype(int)
+    ids = cw.synth_tokens(cw.synth_key(8009, "tf.ids"), 16, cfg.vocab)
+    worst = 0.0
+    for p, t in zip(positions, ids):
+        g_arg = m.step(int(t), int(p))
+        gl = m.logits()
+        ol, _ = o.step(int(t), int(p))
+        diff = float(np.max(np.abs(gl - ol)))
+        top = np.sort(ol)[-2:]
+        print(f"\n[qwen3-8b tf] pos {p} id {t}: max |logit diff| {diff:.3e}, "
+              f"oracle argmax {int(np.argmax(ol))} margin {top[1] - top[0]:.3e}", flush=True)
+        worst = max(worst, diff)
+        assert diff <= LOGIT_TOL, (p, diff)
+        assert g_arg == int(np.argmax(ol)), (p, g_arg, int(np.argmax(ol)))
+    print(f"\n[qwen3-8b tf] worst |logit diff| over 16 positions = {worst:.3e}", flush=True)
+    m.close()
+    o.close()
+
+
 # ---------------------------------------------------------------- fused decode step
 
 # The persistent decode-step kernel raised an illegal memory access on its last

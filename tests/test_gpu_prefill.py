@@ -47,6 +47,38 @@ def test_q4_gemm_vs_oracle(ctx, m, in_f, out_f):
     assert worst <= 1e-4, worst
 
 
+# the four projection shapes of one 8B layer at the 512-token workload:
+# QKV (4096 -> 6144), O (4096 -> 4096), gate/up (4096 -> 12288, each) and
+# down (12288 -> 4096); (m, in_f, out_f).  These run the split-K and tile
+# choices the prefill bench times.
+GEMM_8B_512 = [(512, 4096, 6144), (512, 4096, 4096), (512, 4096, 12288), (512, 12288, 4096)]
+
+
+@pytest.mark.parametrize("m,in_f,out_f", GEMM_8B_512)
+def test_q4_gemm_8b_shapes_at_512(ctx, m, in_f, out_f):
+    """Every element against an f64 product of the exactly dequantized
+    weights (|y - y64| <= 2e-5 * sum_k |w x|, and 1e-4 of max|y| overall);
+    sample rows against the oracle's sequential dot (main.rs:133-150)."""
+    s, q = cw.synth_q4(cw.synth_key(23, f"g{out_f}x{in_f}"), out_f, in_f, 0.02)
+    x = cw.synth_normal_f32(cw.synth_key(23, f"gx{m}x{in_f}"), m * in_f).reshape(m, in_f)
+    y = ctx.q4_gemm(ctx.storage(x), m, ctx.storage(s), ctx.storage(q), in_f, out_f).download()
+    y = y.reshape(m, out_f).astype(np.float64)
+    w = orc.dequant_q4_0_soa(s, q).reshape(out_f, in_f).astype(np.float64)
+    x64 = x.astype(np.float64)
+    y64 = x64 @ w.T
+    bound = np.abs(x64) @ np.abs(w).T
+    err = np.abs(y - y64)
+    worst = np.unravel_index(np.argmax(err / (bound + 1e-30)), err.shape)
+    assert np.all(err <= 2e-5 * bound + 1e-30), (worst, err[worst], bound[worst])
+    rel = float(np.max(err) / np.max(np.abs(y64)))
+    print(f"\n[q4_gemm {m}x{in_f}->{out_f}] max rel err vs f64 {rel:.2e}", flush=True)
+    assert rel <= 1e-4
+    orc.set_threads(16)
+    for i in (0, 1, 63, 64, 127, 128, 255, 256, 383, 511):
+        ref = orc.q4_gemv(x[i], s, q, in_f, out_f)
+        assert rel_err(y[i], ref) <= 1e-4, i
+
+
 def test_q4_gemm_rows_match_gemv(ctx):
     """Every row of the batched GEMM equals the decode GEMV of that row to
     within the same tolerance (two different kernels, one definition)."""
@@ -168,6 +200,44 @@ def test_prefill_qwen3_8b_layers(ctx):
     toks = m.tokens(N)
     ref, _ = o.generate(prompt, N + 1)
     assert np.array_equal(toks, ref[1:N + 1]), (toks, ref[1:N + 1])
+    m.close()
+    o.close()
+
+
+def test_prefill_qwen3_8b_layers_512(ctx):
+    """The benchmarked prompt length: a 512-token batched prefill on two
+    layers of the Qwen3-8B shape (vocab cut to 4096 so the oracle's 512
+    per-token forwards finish quickly).  Causal MFMA attention over 8 query
+    tiles and 512 keys, the M = 512 split-K GEMMs with the in-place residual:
+    last-position logits within 1e-3 of the oracle's per-token loop, the same
+    next token, then 4 greedy steps from the prefilled cache."""
+    P, N = 512, 4
+    cfg = cw.make_config(2, 4096, 32, 8, 128, 12288, 4096, P + N + 1, cw.CW_F16, 1e-6, 1e6)
+    weights = cw.synthetic_weights(cfg, 81)
+    prompt = cw.synth_tokens(cw.synth_key(81, "p512"), P, cfg.vocab)
+    m = cw.Model(ctx, cfg)
+    m.set_weights(weights)
+    m.finalize()
+    orc.set_threads(16)
+    o = orc.OracleModel(cfg, weights)
+    nxt = m.prefill(prompt)
+    gl = m.logits()
+    ref_logits = oracle_prompt_logits(o, prompt)
+    diff = float(np.max(np.abs(gl - ref_logits)))
+    top = np.sort(ref_logits)[-2:]
+    print(f"\n[qwen3-8b x2 layers] prefill {P}: max |logit diff| = {diff:.3e}, "
+          f"oracle top-2 margin {top[1] - top[0]:.3e}", flush=True)
+    assert diff <= LOGIT_TOL, diff
+    assert nxt == int(np.argmax(ref_logits))
+    m.decode_async(N, mode=cw.STEP_GRAPH)
+    toks = m.tokens(N)
+    # the oracle continues from its own cache (rows 0..P-1 written above)
+    ref, t = [], nxt
+    for i in range(N):
+        lg, _ = o.step(int(t), P + i)
+        t = int(np.argmax(lg))
+        ref.append(t)
+    assert np.array_equal(toks, np.array(ref, np.uint32)), (toks, ref)
     m.close()
     o.close()
 
