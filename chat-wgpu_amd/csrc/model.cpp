@@ -106,9 +106,10 @@ struct cw_model {
 
 namespace {
 
-// The persistent decode-step kernel is switched off until the illegal memory
-// access its last GPU run raised is explained; every entry point that would
-// launch it returns CW_ERR_STATE instead.
+// The persistent decode-step kernel is switched off: it raised an illegal
+// memory access on the GPU, and again after its gate|up layout was fixed (the
+// layout the host-side range check now enforces), so a second cause remains
+// unfound.  Every entry point that would launch it returns CW_ERR_STATE.
 constexpr bool kFusedStepDisabled = true;
 
 // Model calls synchronise, allocate or clear memory, none of which may be
@@ -334,8 +335,8 @@ int check_fused(cw_model *m) {
 int run_steps(cw_model *m, int n, int mode) {
     if (mode == CW_STEP_FUSED) {
         if (kFusedStepDisabled) {
-            set_error("fused decode step disabled: its last GPU run raised an illegal memory "
-                      "access whose cause is not yet found (use CW_STEP_GRAPH)");
+            set_error("fused decode step disabled: it raised an illegal memory access on the "
+                      "GPU whose cause is not yet found (use CW_STEP_GRAPH)");
             return CW_ERR_STATE;
         }
         if (m->fused_unsupported) {

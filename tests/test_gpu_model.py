@@ -76,6 +76,21 @@ def test_fused_step_refused_while_disabled(ctx):
     m.close()
 
 
+@pytest.mark.skip(reason="fused decode step disabled: an illegal memory access on the GPU after "
+                         "the gate|up layout fix; second cause not found")
+def test_fused_step_runs_after_the_layout_check(ctx):
+    """CW_STEP_FUSED launches once the host-side range check of its buffer
+    layout has passed at cw_model_finalize: the ids equal the graph path's."""
+    cfg = cw.make_config(2, 256, 4, 2, 128, 512, 1000, 8)
+    m = cw.Model(ctx, cfg)
+    m.load_synthetic(3)
+    m.finalize()
+    g = m.generate(np.array([1, 2], np.uint32), 4, mode=cw.STEP_GRAPH)
+    f = m.generate(np.array([1, 2], np.uint32), 4, mode=cw.STEP_FUSED)
+    assert np.array_equal(f, g), (f, g)
+    m.close()
+
+
 def test_missing_tensor_is_an_error(ctx):
     cfg = cw.make_config(1, 64, 4, 2, 16, 128, 256, 8)
     m = cw.Model(ctx, cfg)
@@ -199,11 +214,16 @@ def test_qwen3_8b_teacher_forced_over_the_decode_range(ctx):
 
 # ---------------------------------------------------------------- fused decode step
 
-# The persistent decode-step kernel raised an illegal memory access on its last
-# GPU run (test_fused_step_small_model[f32, 4 heads / 2 kv]); its cause is not
-# found yet, so the library refuses CW_STEP_FUSED and these tests stay skipped.
-FUSED_SKIP = pytest.mark.skip(reason="fused decode step disabled: unexplained illegal memory "
-                                     "access on its last GPU run")
+# The persistent decode-step kernel raised an illegal memory access here
+# (test_fused_step_small_model[f32, 4 heads / 2 kv]): its gate|up phase read
+# 2 * hidden rows from the gate matrix alone.  Gate and up now share one
+# allocation, and cw_model_finalize checks every range the step touches
+# (tests/test_step_layout.py shows the check refusing the old layout), but the
+# one run after that fix faulted again, so a second cause remains: the library
+# refuses CW_STEP_FUSED and these tests stay skipped.
+FUSED_SKIP = pytest.mark.skip(reason="fused decode step disabled: an illegal memory access on "
+                                     "the GPU after the gate|up layout fix; second cause not found")
+
 
 def small128(max_seq, kv_dtype=cw.CW_F32, n_heads=4, n_kv=2):
     """A small model the fused step covers (head_dim 128)."""
