@@ -5,40 +5,41 @@
 // q_h . k_j) v_j over j < seq, kv head = h / (n_heads / n_kv), scale =
 // hd^-0.5, max-rescaled softmax.
 //
-// Split over the sequence (flash-decoding).  Workgroup (chunk c, kv head g)
-// owns CP consecutive positions and one wave per query head of the GQA group:
-//   1. the query, then the K rows, then the V rows of the chunk (this kv
-//      head's slice) are loaded with coalesced 16-byte loads, all issued up
-//      front in the order they are used, into LDS tiles with a 16-byte row
-//      pad (conflict-free row reads);
-//   2. wave j: lane = position, full q.k dot from the K tile against the
-//      query broadcast from LDS (f16 keys feed v_fma_mix directly) while the
-//      V rows are still arriving; wavefront max / sum give the chunk's
-//      softmax partial;
-//   3. wave j: lane = head dimension, P.V over its 1/HPK of the V tile's rows
-//      for every head of the group (each V row leaves LDS once), the waves'
-//      sums added through LDS.
-// No cross-lane reduction is needed per position.  A chunk partial
-// (max, sum, unnormalised o) goes to memory unless the sequence fits one
-// chunk, in which case the normalised output is written directly.  The last
-// workgroup of a kv head to finish (one agent-scope counter per kv head)
-// merges that head group's partials in the same launch, so the merge costs
-// no kernel boundary.  (Scores on the matrix cores were tried for the 4-head
-// groups of the 8B shape: with 4 of 16 MFMA rows used and q / p split into
-// f16 pairs per lane, the kernel ran slower.)
+// Split over the sequence (flash-decoding): a workgroup owns one kv head and a
+// chunk of consecutive positions and writes one chunk partial (max, sum,
+// unnormalised o per query head), unless the sequence fits one chunk, in
+// which case it writes the normalised output.  The last workgroup of a kv head
+// to finish (one agent-scope counter per kv head) merges that head group's
+// partials in the same launch (merge_chunks), so the merge costs no kernel
+// boundary.  Three kernels, by cache type and head size:
+//   * attn_mfma_kernel (f16 cache, head_dim 128: the 8B decode workload):
+//     waves of 16 positions with K and V in registers as loaded; scores and
+//     P.V on the matrix cores with exact f16 operands (K, V as stored; q and
+//     p split into f16 hi + lo), the W wave partials merged in LDS;
+//   * attn_wave_kernel (f32 cache, head_dim 128): the same wave split with
+//     scores and P.V on the vector ALUs;
+//   * attn_kernel (other head sizes): K/V tiles in LDS, lane = position for
+//     the scores, lane = dimension for P.V.
+// Every kernel issues its global loads as straight-line code in the order
+// they are used, and synchronises the workgroup on LDS data only while K/V
+// rows are in flight: a __syncthreads fence, or a load under a branch,
+// makes the compiler wait for every outstanding load first.
 //
 // Coherence across the 8 XCDs (one L2 each): partials are written with
-// write-through (sc1) stores and read with sc1 loads, which miss any line an
-// L2 still holds from an earlier call; a workgroup's stores are complete
-// (s_waitcnt) before its counter increment, and the merging workgroup reads
-// only after its own increment returned.  The merger resets the counter, so
-// every launch, eager or replayed from a graph, starts from zero.
+// write-through (agent-scope, sc1) stores and read with sc1 loads, which miss
+// any line an L2 still holds from an earlier call.  Every wave waits for its
+// own partial stores to be acknowledged (s_waitcnt vmcnt(0): an acknowledged
+// sc1 store has reached the memory side, where every XCD reads), then the
+// workgroup barrier, then one agent-scope atomic increment; the merging
+// workgroup's sc1 loads are issued only after its own increment returned the
+// final count, so they observe every partial.  The merger resets the counter,
+// so every launch, eager or replayed from a graph, starts from zero.
 //
 // Fused prologue (decode step): the raw q/k/v come straight from the fused
 // QKV projection; the kernel applies the per-head QK RMSNorm (norm.wgsl,
 // qwen3.rs:154-155) and RoPE (rope.wgsl), and the workgroup whose chunk holds
-// the new position writes k/v into the cache (cache.rs:21-24) and into its
-// own tile.
+// the new position writes k/v into the cache (cache.rs:21-24) and uses them
+// in place of what its loads read there.
 
 #include <cmath>
 #include <map>
@@ -75,13 +76,6 @@ struct Cfg {
     static constexpr int MAXC = kMaxChunkSpan / CP;
     static constexpr int LDS_MAIN = 2 * CP * ROWP + HPK * HD * 4 + HPK * CP * 4;
     static constexpr int LDS = LDS_MAIN > HPK * MAXC * 4 ? LDS_MAIN : HPK * MAXC * 4;
-    // merge: float4 columns per partial row, chunk slices per wave, partial
-    // rows in flight per lane (one round covers MSL * MB chunks: 36 at
-    // head_dim 128, at most 18 float4 registers)
-    static constexpr int MU = HD / 4;
-    static constexpr int MSL = 64 / MU;
-    static constexpr int MB0 = 36 / MSL > 4 ? 36 / MSL : 4;
-    static constexpr int MB = MB0 < 18 ? MB0 : 18;
     static_assert(LDS <= 160 * 1024, "attention tile exceeds the CU's LDS");
     static_assert(CP >= 8 && CP % 8 == 0, "chunk must hold whole load groups");
     static_assert((CP / HPK) % 4 == 0, "every wave's P.V rows come in fours");
@@ -129,6 +123,16 @@ __device__ __forceinline__ void drain() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// LDS written by some lanes of this wave is read by others: DS operations of
+// one wave execute in order, so keeping the compiler from moving the accesses
+// across this point (and waiting for the writes) is enough
+__device__ __forceinline__ void wave_lds_sync() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 template <typename T>
 __device__ __forceinline__ T to_kv(float v) {
     return (T)v;  // f32 -> f16 rounds to nearest even
@@ -159,6 +163,98 @@ __device__ __forceinline__ float dot16<float>(uint4 k, const float *q, float acc
     acc = __builtin_fmaf(__builtin_bit_cast(float, k.z), q[2], acc);
     acc = __builtin_fmaf(__builtin_bit_cast(float, k.w), q[3], acc);
     return acc;
+}
+
+// Merge of query head h over its n_chunks chunk partials (one wave): the
+// (max, sum) pairs of chunks lane and lane + 64 and the first MB partial rows
+// are all requested before anything waits; lane (slice sl, float4 column e4)
+// takes chunks sl, sl + MSL, ...  Partials are read with sc1 loads (past any
+// L2 line an earlier call left); wl is this wave's own LDS row of MAXC chunk
+// weights, so only a wave-level fence orders its writes and reads.
+template <int HD, int MAXC>
+__device__ __forceinline__ void merge_chunks(const cwi::AttnArgs &a, int h, int n_chunks,
+                                             int max_chunks, float *wl, int lane) {
+    constexpr int MU = HD / 4;        // float4 columns per partial row
+    constexpr int MSL = 64 / MU;      // chunk slices per wave
+    // partial rows in flight per lane: one round covers MSL * MB chunks (36 at
+    // head_dim 128), at most 18 float4 registers
+    constexpr int MB0 = 36 / MSL > 4 ? 36 / MSL : 4;
+    constexpr int MB = MB0 < 18 ? MB0 : 18;
+    float *const part_ml = a.part + (size_t)a.n_heads * max_chunks * HD;
+    const int e4 = lane % MU, sl = lane / MU;
+    const __amdgpu_buffer_rsrc_t rp =
+        make_rsrc(a.part + (size_t)h * max_chunks * HD, (uint32_t)(n_chunks * HD * 4));
+    const __amdgpu_buffer_rsrc_t rm =
+        make_rsrc(part_ml + (size_t)h * max_chunks * 2, (uint32_t)(n_chunks * 8));
+    // (the loads are read through bit casts to float vectors: element access
+    // on the builtins' integer results does not give the loaded dwords)
+    const float2 ml_a = ld_pair(rm, lane);
+    const float2 ml_b = ld_pair(rm, lane + 64);
+    // whole byte offsets in the vector offset, which the buffer range check
+    // covers: rows past n_chunks read as zeros
+    const uint32_t voff = (uint32_t)((sl * HD + 4 * e4) * 4);
+    float4 v[MB];
+#pragma unroll
+    for (int u = 0; u < MB; ++u)
+        v[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rp, voff + MSL * u * HD * 4, 0, kSc1));
+    const float m_a = ml_a.x, l_a = ml_a.y, m_b = ml_b.x, l_b = ml_b.y;
+    float mx = fmaxf(lane < n_chunks ? m_a : -INFINITY, lane + 64 < n_chunks ? m_b : -INFINITY);
+    for (int cc = lane + 128; cc < n_chunks; cc += 64) mx = fmaxf(mx, ld_pair(rm, cc).x);
+    const float M = wave_max(mx);
+    float ls = 0.0f;
+    if (lane < n_chunks) {
+        const float f = expf(m_a - M);
+        wl[lane] = f;
+        ls = f * l_a;
+    }
+    if (lane + 64 < n_chunks) {
+        const float f = expf(m_b - M);
+        wl[lane + 64] = f;
+        ls += f * l_b;
+    }
+    for (int cc = lane + 128; cc < n_chunks; cc += 64) {
+        const float2 ml = ld_pair(rm, cc);
+        const float f = expf(ml.x - M);
+        wl[cc] = f;
+        ls += f * ml.y;
+    }
+    const float L = wave_sum(ls);
+    wave_lds_sync();  // the weights are in LDS
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    auto fold = [&](int cc, float4 x) {
+        const float f = cc < n_chunks ? wl[cc] : 0.0f;
+        acc.x = __builtin_fmaf(f, x.x, acc.x);
+        acc.y = __builtin_fmaf(f, x.y, acc.y);
+        acc.z = __builtin_fmaf(f, x.z, acc.z);
+        acc.w = __builtin_fmaf(f, x.w, acc.w);
+    };
+#pragma unroll
+    for (int u = 0; u < MB; ++u) fold(sl + MSL * u, v[u]);
+    // chunks beyond the first round (long caches): rounds of 8 rows per lane
+#pragma unroll 1
+    for (int cc0 = MSL * MB; cc0 < n_chunks; cc0 += MSL * 8) {
+        float4 t[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            t[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rp, voff + (cc0 + MSL * u) * HD * 4, 0, kSc1));
+#pragma unroll
+        for (int u = 0; u < 8; ++u) fold(cc0 + sl + MSL * u, t[u]);
+    }
+    // combine the chunk slices (lanes e4 + MU * s) of each column
+#pragma unroll
+    for (int off = MU; off < 64; off <<= 1) {
+        acc.x += __shfl_xor(acc.x, off);
+        acc.y += __shfl_xor(acc.y, off);
+        acc.z += __shfl_xor(acc.z, off);
+        acc.w += __shfl_xor(acc.w, off);
+    }
+    if (sl == 0) {
+        const float inv = 1.0f / L;
+        *reinterpret_cast<float4 *>(a.out + (size_t)h * HD + 4 * e4) =
+            make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+    }
 }
 
 template <typename KVT, int HD, int HPK>
@@ -539,88 +635,794 @@ __global__ __launch_bounds__(64 * HPK) void attn_kernel(cwi::AttnArgs a, float s
     __syncthreads();
     if (!last_s) return;
 
-    // ---- 8. merge of head h over the n_chunks partials (wave = head):
-    // lane (slice sl, float4 column e4) takes chunks sl, sl + MSL, ...; the
-    // (max, sum) pairs of chunks lane and lane + 64 and the first MB partial
-    // rows are all requested before anything waits ----
-    constexpr int MU = C::MU, MSL = C::MSL, MB = C::MB;
-    const int e4 = lane % MU, sl = lane / MU;
-    const __amdgpu_buffer_rsrc_t rp =
-        make_rsrc(a.part + (size_t)h * max_chunks * HD, (uint32_t)(n_chunks * HD * 4));
-    const __amdgpu_buffer_rsrc_t rm =
-        make_rsrc(part_ml + (size_t)h * max_chunks * 2, (uint32_t)(n_chunks * 8));
-    // (the loads are read through bit casts to float vectors: element access
-    // on the builtins' integer results does not give the loaded dwords)
-    const float2 ml_a = ld_pair(rm, lane);
-    const float2 ml_b = ld_pair(rm, lane + 64);
-    // whole byte offsets in the vector offset, which the buffer range check
-    // covers: rows past n_chunks read as zeros
-    const uint32_t voff = (uint32_t)((sl * HD + 4 * e4) * 4);
-    float4 v[MB];
+    // ---- 8. merge of head h over the n_chunks partials (wave = head) ----
+    merge_chunks<HD, C::MAXC>(a, h, n_chunks, max_chunks,
+                              reinterpret_cast<float *>(lds) + wave * C::MAXC, lane);
+}
+
+// ---------------------------------------------------------------- head_dim 128
+
+// Decode attention for head_dim 128 with the K/V rows kept in registers as
+// they were loaded: workgroup (chunk c, kv head g) has W waves, wave w owns
+// the PW = 16 positions c*CP + 16w ...  A lane holds, for NR rows of its
+// slice, one 16-byte unit of the row (EPU elements): the loads are plain
+// coalesced row reads, and no LDS tile or workgroup barrier sits between a
+// wave's data arriving and its compute, so each wave computes as soon as its
+// own rows are in.
+//   scores: per (row, head) a partial dot over the lane's EPU dims, summed
+//     over the U4_ROW lanes of the row with DPP (every lane gets the sum);
+//   softmax: per head over the wave's 16 positions;
+//   P.V: the lane's rows times their p, summed over the row groups;
+// the W wave partials meet in LDS; the workgroup writes one chunk partial
+// (or the output, for a single chunk) and the last workgroup of the kv head
+// merges the chunks (merge_chunks).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// sum over aligned groups of G lanes (16 or 32); every lane gets its group's sum
+template <int G>
+__device__ __forceinline__ float row_group_sum(float v) {
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);  // row_half_mirror
+    v += dpp_f<0x140>(v);  // row_mirror
+    if constexpr (G >= 32) v += __shfl_xor(v, 16);
+    return v;
+}
+
+template <typename KVT, int HPK, int W>
+struct WaveCfg {
+    static constexpr int HD = 128;
+    static constexpr int HALF = HD / 2;             // = 64: one (lo, hi) pair per lane
+    static constexpr int ES = (int)sizeof(KVT);
+    static constexpr int EPU = 16 / ES;             // elements per 16-byte unit
+    static constexpr int U4_ROW = HD / EPU;         // lanes per row: 16 (f16), 32 (f32)
+    static constexpr int RPL = 64 / U4_ROW;         // rows per wave load
+    static constexpr int PW = 16;                   // positions per wave
+    static constexpr int NR = PW / RPL;             // rows per lane
+    static constexpr int CP = PW * W;               // positions per workgroup
+    static constexpr int THREADS = 64 * W;
+    static constexpr int ROWB = HD * ES;
+    static constexpr int MAXC = kMaxChunkSpan / CP;
+    // LDS (floats): q [HPK][HD]; the new k and v [2][HD]; the wave partials
+    // [W][HPK][HD + 2], whose space the chunk merge's weights [HPK][MAXC] reuse
+    static constexpr int Q_F = HPK * HD;
+    static constexpr int NEW_F = 2 * HD;
+    static constexpr int WP_F = W * HPK * (HD + 2);
+    static constexpr int CW_F = HPK * MAXC;
+    static constexpr int LDS = (Q_F + NEW_F + (WP_F > CW_F ? WP_F : CW_F)) * 4;
+    static_assert(W >= HPK, "the chunk merge takes one wave per query head");
+    static_assert(LDS <= 64 * 1024, "attention LDS");
+};
+
+// EPU elements of a 16-byte unit as f32
+template <typename KVT>
+__device__ __forceinline__ void unpack16(uint4 w, float *out);
+template <>
+__device__ __forceinline__ void unpack16<_Float16>(uint4 w, float *out) {
+    const uint32_t d[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-    for (int u = 0; u < MB; ++u)
-        v[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                              rp, voff + MSL * u * HD * 4, 0, kSc1));
-    const float m_a = ml_a.x, l_a = ml_a.y, m_b = ml_b.x, l_b = ml_b.y;
-    float mx = fmaxf(lane < n_chunks ? m_a : -INFINITY, lane + 64 < n_chunks ? m_b : -INFINITY);
-    for (int cc = lane + 128; cc < n_chunks; cc += 64) {
-        mx = fmaxf(mx, ld_pair(rm, cc).x);
+    for (int i = 0; i < 4; ++i) {
+        const half2v h = __builtin_bit_cast(half2v, d[i]);
+        out[2 * i] = (float)h.x;
+        out[2 * i + 1] = (float)h.y;
     }
-    const float M = wave_max(mx);
-    float *wl = reinterpret_cast<float *>(lds) + wave * C::MAXC;  // tiles are no longer read
-    float ls = 0.0f;
-    if (lane < n_chunks) {
-        const float f = expf(m_a - M);
-        wl[lane] = f;
-        ls = f * l_a;
+}
+template <>
+__device__ __forceinline__ void unpack16<float>(uint4 w, float *out) {
+    out[0] = __builtin_bit_cast(float, w.x);
+    out[1] = __builtin_bit_cast(float, w.y);
+    out[2] = __builtin_bit_cast(float, w.z);
+    out[3] = __builtin_bit_cast(float, w.w);
+}
+
+// EPU f32 values (exactly representable in KVT) packed into a 16-byte unit
+template <typename KVT>
+__device__ __forceinline__ uint4 pack16(const float *v);
+template <>
+__device__ __forceinline__ uint4 pack16<_Float16>(const float *v) {
+    uint32_t d[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        half2v h;
+        h.x = (_Float16)v[2 * i];
+        h.y = (_Float16)v[2 * i + 1];
+        d[i] = __builtin_bit_cast(uint32_t, h);
     }
-    if (lane + 64 < n_chunks) {
-        const float f = expf(m_b - M);
-        wl[lane + 64] = f;
-        ls += f * l_b;
-    }
-    for (int cc = lane + 128; cc < n_chunks; cc += 64) {
-        const float2 ml = ld_pair(rm, cc);
-        const float f = expf(ml.x - M);
-        wl[cc] = f;
-        ls += f * ml.y;
-    }
-    const float L = wave_sum(ls);
-    __syncthreads();  // the weights are in LDS
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    auto fold = [&](int cc, float4 x) {
-        const float f = cc < n_chunks ? wl[cc] : 0.0f;
-        acc.x = __builtin_fmaf(f, x.x, acc.x);
-        acc.y = __builtin_fmaf(f, x.y, acc.y);
-        acc.z = __builtin_fmaf(f, x.z, acc.z);
-        acc.w = __builtin_fmaf(f, x.w, acc.w);
+    return make_uint4(d[0], d[1], d[2], d[3]);
+}
+template <>
+__device__ __forceinline__ uint4 pack16<float>(const float *v) {
+    return make_uint4(__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
+                      __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3]));
+}
+
+// workgroup barrier for LDS data only: the LDS writes are waited for, but not
+// the global loads still in flight (a __syncthreads fence would wait for those
+// too, so no wave could compute while its K/V rows arrive)
+__device__ __forceinline__ void lds_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+template <typename KVT, int HPK, int W, bool FUSED>
+__global__ __launch_bounds__(64 * W) void attn_wave_kernel(cwi::AttnArgs a, float scale,
+                                                           int max_chunks) {
+    using C = WaveCfg<KVT, HPK, W>;
+    constexpr int HD = C::HD, HALF = C::HALF, EPU = C::EPU, NR = C::NR;
+    extern __shared__ float lds_f[];
+    float *q_s = lds_f;              // [HPK][HD]
+    float *new_s = q_s + C::Q_F;     // new k [HD], new v [HD]
+    float *wp = new_s + C::NEW_F;    // [W][HPK][HD + 2]
+
+    const int c = blockIdx.x, g = blockIdx.y;
+    const int seq = a.pos_dev ? (*a.pos_dev + 1) : a.seq;
+    const int c0 = c * C::CP;
+    if (c0 >= seq) return;
+    const int n_chunks = (seq + C::CP - 1) / C::CP;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kv_dim = a.n_kv * HD;
+    const int pos_new = seq - 1;
+    const int w0 = c0 + wave * C::PW;  // this wave's first position
+    const bool live = w0 < seq;        // (wave-uniform, like w_new)
+    const bool w_new = FUSED && pos_new >= w0 && pos_new < w0 + C::PW;
+    unsigned char *kc = reinterpret_cast<unsigned char *>(a.k_cache);
+    unsigned char *vc = reinterpret_cast<unsigned char *>(a.v_cache);
+    const size_t row_bytes = (size_t)kv_dim * C::ES;
+    const int rg = lane / C::U4_ROW, u = lane % C::U4_ROW;  // row of a load, unit of the row
+
+    // ---- 1. loads, all of them straight-line (a load under a branch makes
+    // the compiler wait for every load at the join), in the order they are
+    // used: a query head (head g*HPK + wave, clamped; only waves below HPK
+    // use it), the new k and v and their RoPE row (used by the wave holding
+    // pos_new), then this wave's K rows and V rows (rows past the sequence
+    // clamped to its last row and masked later) ----
+    const int h = g * HPK + (wave < HPK ? wave : HPK - 1);
+    const bool q_wave = wave < HPK;
+    // a wave that does not use a vector still issues its load, over a buffer
+    // range of 0 bytes: no memory request, zeros back, straight-line code
+    auto rs = [](const float *p, bool use) {
+        return make_rsrc(p, use ? (uint32_t)(HD * sizeof(float)) : 0u);
     };
-#pragma unroll
-    for (int u = 0; u < MB; ++u) fold(sl + MSL * u, v[u]);
-    // chunks beyond the first round (long caches): rounds of 8 rows per lane
-#pragma unroll 1
-    for (int cc0 = MSL * MB; cc0 < n_chunks; cc0 += MSL * 8) {
-        float4 t[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-            t[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                  rp, voff + (cc0 + MSL * u) * HD * 4, 0, kSc1));
-#pragma unroll
-        for (int u = 0; u < 8; ++u) fold(cc0 + sl + MSL * u, t[u]);
+    auto ld2 = [&](__amdgpu_buffer_rsrc_t r, float &x0, float &x1) {
+        x0 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, lane * 4, 0, 0));
+        x1 = __builtin_bit_cast(float,
+                                __builtin_amdgcn_raw_buffer_load_b32(r, (lane + HALF) * 4, 0, 0));
+    };
+    float lo, hi, gl = 0.f, gh = 0.f, cs = 0.f, sn = 0.f;
+    float klo = 0.f, khi = 0.f, kgl = 0.f, kgh = 0.f, v0 = 0.f, v1 = 0.f;
+    if constexpr (FUSED) {
+        const int q_dim = a.n_heads * HD;
+        const float *ks = a.qkv + q_dim + g * HD;
+        ld2(rs(a.qkv + (size_t)h * HD, q_wave), lo, hi);
+        ld2(rs(a.q_norm_w, q_wave), gl, gh);
+        // the RoPE row of pos_new as [cos (64) | sin (64)] through two ranges
+        const __amdgpu_buffer_rsrc_t rc =
+            make_rsrc(a.cos_t + (size_t)pos_new * HALF, (q_wave || w_new) ? HALF * 4 : 0u);
+        const __amdgpu_buffer_rsrc_t rsn =
+            make_rsrc(a.sin_t + (size_t)pos_new * HALF, (q_wave || w_new) ? HALF * 4 : 0u);
+        cs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rc, lane * 4, 0, 0));
+        sn = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsn, lane * 4, 0, 0));
+        ld2(rs(ks, w_new), klo, khi);
+        ld2(rs(a.k_norm_w, w_new), kgl, kgh);
+        ld2(rs(ks + kv_dim, w_new), v0, v1);
+    } else {
+        ld2(rs(a.q + (size_t)h * HD, q_wave), lo, hi);
     }
-    // combine the chunk slices (lanes e4 + MU * s) of each column
+    // keep the issue order: the scheduler would otherwise sink the small
+    // loads below the rows, and waiting for them would wait for the rows too
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 kr[NR], vr[NR];
 #pragma unroll
-    for (int off = MU; off < 64; off <<= 1) {
-        acc.x += __shfl_xor(acc.x, off);
-        acc.y += __shfl_xor(acc.y, off);
-        acc.z += __shfl_xor(acc.z, off);
-        acc.w += __shfl_xor(acc.w, off);
+    for (int i = 0; i < NR; ++i) {
+        int p = w0 + i * C::RPL + rg;
+        p = p < seq ? p : seq - 1;
+        const size_t off = (size_t)p * row_bytes + (size_t)g * C::ROWB + (size_t)u * 16;
+        kr[i] = *reinterpret_cast<const uint4 *>(kc + off);
     }
-    if (sl == 0) {
-        const float inv = 1.0f / L;
-        *reinterpret_cast<float4 *>(a.out + (size_t)h * HD + 4 * e4) =
-            make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        int p = w0 + i * C::RPL + rg;
+        p = p < seq ? p : seq - 1;
+        const size_t off = (size_t)p * row_bytes + (size_t)g * C::ROWB + (size_t)u * 16;
+        vr[i] = *reinterpret_cast<const uint4 *>(vc + off);
     }
+
+    // ---- 2. query head of waves below HPK (normalised + rotated when fused) ----
+    if (wave < HPK) {
+        float r0 = lo, r1 = hi;
+        if constexpr (FUSED) {
+            const float ss = wave_sum(lo * lo + hi * hi);
+            const float inv = 1.0f / sqrtf(ss / (float)HD + a.eps);
+            const float l0 = (lo * inv) * gl;
+            const float h0 = (hi * inv) * gh;
+            r0 = l0 * cs - h0 * sn;
+            r1 = h0 * cs + l0 * sn;
+            if (a.q_tap && c == 0) {  // the "q" tap (qwen3.rs:165)
+                a.q_tap[(size_t)h * HD + lane] = r0;
+                a.q_tap[(size_t)h * HD + lane + HALF] = r1;
+            }
+        }
+        q_s[wave * HD + lane] = r0;
+        q_s[wave * HD + lane + HALF] = r1;
+    }
+
+    // ---- 3. the new position's k (normalised + rotated) and v: to the cache
+    // (cache.rs:21-24) and to LDS, from where the lanes holding that row take
+    // them in place of what their loads read ----
+    if (w_new) {
+        const float kss = wave_sum(klo * klo + khi * khi);
+        const float kinv = 1.0f / sqrtf(kss / (float)HD + a.eps);
+        const float l0 = (klo * kinv) * kgl;
+        const float h0 = (khi * kinv) * kgh;
+        const KVT k0 = to_kv<KVT>(l0 * cs - h0 * sn), k1 = to_kv<KVT>(h0 * cs + l0 * sn);
+        const KVT vv0 = to_kv<KVT>(v0), vv1 = to_kv<KVT>(v1);
+        KVT *kg = reinterpret_cast<KVT *>(kc + (size_t)pos_new * row_bytes + (size_t)g * C::ROWB);
+        KVT *vg = reinterpret_cast<KVT *>(vc + (size_t)pos_new * row_bytes + (size_t)g * C::ROWB);
+        kg[lane] = k0;
+        kg[lane + HALF] = k1;
+        vg[lane] = vv0;
+        vg[lane + HALF] = vv1;
+        new_s[lane] = (float)k0;
+        new_s[lane + HALF] = (float)k1;
+        new_s[HD + lane] = (float)vv0;
+        new_s[HD + lane + HALF] = (float)vv1;
+    }
+    lds_barrier();  // q (and the new row) are in LDS
+    if (w_new) {
+        float kn[EPU], vn[EPU];
+#pragma unroll
+        for (int e = 0; e < EPU; ++e) {
+            kn[e] = new_s[u * EPU + e];
+            vn[e] = new_s[HD + u * EPU + e];
+        }
+        const uint4 kp = pack16<KVT>(kn), vp = pack16<KVT>(vn);
+        const int r = pos_new - w0;
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            const bool mine = i * C::RPL + rg == r;
+            kr[i].x = mine ? kp.x : kr[i].x;
+            kr[i].y = mine ? kp.y : kr[i].y;
+            kr[i].z = mine ? kp.z : kr[i].z;
+            kr[i].w = mine ? kp.w : kr[i].w;
+            vr[i].x = mine ? vp.x : vr[i].x;
+            vr[i].y = mine ? vp.y : vr[i].y;
+            vr[i].z = mine ? vp.z : vr[i].z;
+            vr[i].w = mine ? vp.w : vr[i].w;
+        }
+    }
+
+    float o[HPK][EPU], m[HPK], l[HPK];
+    if (live) {
+        // ---- 4. scores: partial dots over the lane's EPU dims, summed over
+        // the U4_ROW lanes of each row ----
+        float sc[NR][HPK];
+#pragma unroll
+        for (int hh = 0; hh < HPK; ++hh) {
+            float qv[EPU];
+#pragma unroll
+            for (int e = 0; e < EPU; e += 4) {
+                const float4 q4 = *reinterpret_cast<const float4 *>(q_s + hh * HD + u * EPU + e);
+                qv[e] = q4.x;
+                qv[e + 1] = q4.y;
+                qv[e + 2] = q4.z;
+                qv[e + 3] = q4.w;
+            }
+#pragma unroll
+            for (int i = 0; i < NR; ++i) sc[i][hh] = dot16<KVT>(kr[i], qv, 0.0f);
+        }
+#pragma unroll
+        for (int i = 0; i < NR; ++i)
+#pragma unroll
+            for (int hh = 0; hh < HPK; ++hh) sc[i][hh] = row_group_sum<C::U4_ROW>(sc[i][hh]);
+
+        // ---- 5. softmax partial per head over the wave's positions ----
+#pragma unroll
+        for (int hh = 0; hh < HPK; ++hh) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < NR; ++i) {
+                const bool in = w0 + i * C::RPL + rg < seq;
+                sc[i][hh] = in ? sc[i][hh] * scale : -INFINITY;
+                mx = fmaxf(mx, sc[i][hh]);
+            }
+#pragma unroll
+            for (int off = C::U4_ROW; off < 64; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+            float ls = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NR; ++i) {
+                const float pr = sc[i][hh] == -INFINITY ? 0.0f : expf(sc[i][hh] - mx);
+                sc[i][hh] = pr;
+                ls += pr;
+            }
+#pragma unroll
+            for (int off = C::U4_ROW; off < 64; off <<= 1) ls += __shfl_xor(ls, off);
+            m[hh] = mx;
+            l[hh] = ls;
+        }
+
+        // ---- 6. P.V over the lane's rows, summed over the row groups ----
+#pragma unroll
+        for (int hh = 0; hh < HPK; ++hh)
+#pragma unroll
+            for (int e = 0; e < EPU; ++e) o[hh][e] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            float vv[EPU];
+            unpack16<KVT>(vr[i], vv);
+#pragma unroll
+            for (int hh = 0; hh < HPK; ++hh)
+#pragma unroll
+                for (int e = 0; e < EPU; ++e) o[hh][e] = __builtin_fmaf(sc[i][hh], vv[e], o[hh][e]);
+        }
+#pragma unroll
+        for (int off = C::U4_ROW; off < 64; off <<= 1)
+#pragma unroll
+            for (int hh = 0; hh < HPK; ++hh)
+#pragma unroll
+                for (int e = 0; e < EPU; ++e) o[hh][e] += __shfl_xor(o[hh][e], off);
+    } else {
+#pragma unroll
+        for (int hh = 0; hh < HPK; ++hh) {
+            m[hh] = -INFINITY;
+            l[hh] = 0.0f;
+#pragma unroll
+            for (int e = 0; e < EPU; ++e) o[hh][e] = 0.0f;
+        }
+    }
+
+    // ---- 7. the wave's partial (o, m, l) per head into LDS ----
+    if (rg == 0) {
+#pragma unroll
+        for (int hh = 0; hh < HPK; ++hh) {
+            float *dst = wp + (wave * HPK + hh) * (HD + 2);
+#pragma unroll
+            for (int e = 0; e < EPU; ++e) dst[u * EPU + e] = o[hh][e];
+            if (u == 0) {
+                dst[HD] = m[hh];
+                dst[HD + 1] = l[hh];
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- 8. merge of the W wave partials: thread -> (head, dim); the chunk
+    // partial goes to memory write-through, or the output when the sequence
+    // is one chunk ----
+    float *const part_ml = a.part + (size_t)a.n_heads * max_chunks * HD;
+    for (int idx = tid; idx < HPK * HD; idx += C::THREADS) {
+        const int hh = idx / HD, d = idx % HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < W; ++w) M = fmaxf(M, wp[(w * HPK + hh) * (HD + 2) + HD]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const float *src = wp + (w * HPK + hh) * (HD + 2);
+            const float f = src[HD] == -INFINITY ? 0.0f : expf(src[HD] - M);
+            L = __builtin_fmaf(f, src[HD + 1], L);
+            O = __builtin_fmaf(f, src[d], O);
+        }
+        const int hg = g * HPK + hh;
+        if (n_chunks == 1) {
+            a.out[(size_t)hg * HD + d] = O / L;
+        } else {
+            st_part(a.part + ((size_t)hg * max_chunks + c) * HD + d, O);
+            if (d == 0) {
+                float *pml = part_ml + ((size_t)hg * max_chunks + c) * 2;
+                st_part(pml, M);
+                st_part(pml + 1, L);
+            }
+        }
+    }
+    if (n_chunks == 1) return;
+
+    // ---- 9. arrival: every wave's partial stores are complete (s_waitcnt),
+    // then one increment of this kv head's counter; the last arriver merges
+    // the chunks, one wave per query head ----
+    __shared__ int last_s;
+    drain();
+    __syncthreads();
+    if (tid == 0) {
+        unsigned *cnt = a.cnt + 32 * g;
+        const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = old + 1 == (unsigned)n_chunks;
+        if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_s = last;
+    }
+    __syncthreads();
+    if (!last_s) return;
+    if (wave < HPK)
+        merge_chunks<HD, C::MAXC>(a, g * HPK + wave, n_chunks, max_chunks, wp + wave * C::MAXC,
+                                  lane);
+}
+
+// ---------------------------------------------------------------- f16 cache, head_dim 128: scores on MFMA
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Workgroup (chunk c, kv head g) with W waves (W = blockDim / 64, a launch
+// choice), wave w owning the 16 positions c*16W + 16w ...  Per wave:
+//   scores S^T[key][head] = K q^T on v_mfma_f32_16x16x32_f16: lane l holds
+//     A[l % 16][8 (l / 16) + j] and B[8 (l / 16) + j][l % 16] and receives
+//     D[4 (l / 16) + r][l % 16].  A is K row l % 16 (the wave's key), B is
+//     q^T (column = query head, HPK of 16 used).  The k order only has to
+//     agree between A and B, so in step t lane l takes dims 32 (l / 16) + 8t
+//     .. + 8: its four steps read 64 contiguous bytes of its key row.  K is
+//     f16 in the cache and enters exactly; q is split into f16 hi + lo (two
+//     MFMAs per step), so the products are those of f32 q to ~22 bits, summed
+//     in f32;
+//   softmax per head over the 16 keys on the lanes holding that head's
+//     column; p goes through a 16 x HPK LDS tile of the wave;
+//   P.V on the vector ALUs: V rows in their natural layout (lane = 16-byte
+//     unit of a row, row group = l / 16), summed over the row groups.
+// The W wave partials merge in LDS, the chunk partial goes to memory (or
+// the output for a single chunk), and the last workgroup of the kv head
+// merges the chunks (merge_chunks).
+template <int HPK>
+struct MfmaCfg {
+    static constexpr int HD = 128, HALF = 64;
+    // waves per workgroup at most (8 for 8-head groups, whose accumulators
+    // need the registers of 2 waves per SIMD)
+    static constexpr int WMAX = HPK >= 8 ? 8 : 16;
+    static constexpr int PW = 16;                   // positions per wave
+    static constexpr int ROWB = HD * 2;             // f16 row slice of one kv head
+    static constexpr int MAXC = kMaxChunkSpan / (PW * HPK);  // chunks at the smallest W = HPK
+    // LDS (bytes): q hi/lo f16 [2][HPK][HD]; new k, v f32 [2][HD]; p per wave
+    // f32 [WMAX][16][HPK]; wave partials f32 [WMAX][HPK][HD + 2], reused for
+    // the chunk weights [HPK][MAXC]
+    static constexpr int Q16_B = 2 * HPK * HD * 2;
+    static constexpr int NEW_B = 2 * HD * 4;
+    static constexpr int P_B = WMAX * PW * HPK * 4;
+    static constexpr int WP_B0 = WMAX * HPK * (HD + 2) * 4;
+    static constexpr int CW_B = HPK * MAXC * 4;
+    static constexpr int WP_B = WP_B0 > CW_B ? WP_B0 : CW_B;
+    static constexpr int LDS = Q16_B + NEW_B + P_B + WP_B;
+    static_assert(LDS <= 160 * 1024, "attention LDS");
+    static_assert(HPK <= 16, "query heads of a kv head fit the MFMA columns");
+};
+
+template <int HPK, bool FUSED>
+__global__ __launch_bounds__(64 * MfmaCfg<HPK>::WMAX) void attn_mfma_kernel(cwi::AttnArgs a,
+                                                                             float scale,
+                                                                             int max_chunks) {
+    using C = MfmaCfg<HPK>;
+    constexpr int HD = C::HD, HALF = C::HALF;
+    extern __shared__ float4 lds_mf[];
+    unsigned char *lds = reinterpret_cast<unsigned char *>(lds_mf);
+    _Float16 *q16 = reinterpret_cast<_Float16 *>(lds);              // [2][HPK][HD]
+    float *new_s = reinterpret_cast<float *>(lds + C::Q16_B);       // [2][HD]
+    float *p_all = reinterpret_cast<float *>(lds + C::Q16_B + C::NEW_B);  // [WMAX][16][HPK]
+    float *wp = reinterpret_cast<float *>(lds + C::Q16_B + C::NEW_B + C::P_B);
+
+    const int W = blockDim.x >> 6;
+    const int CP = C::PW * W;
+    const int c = blockIdx.x, g = blockIdx.y;
+    const int seq = a.pos_dev ? (*a.pos_dev + 1) : a.seq;
+    const int c0 = c * CP;
+    if (c0 >= seq) return;
+    const int n_chunks = (seq + CP - 1) / CP;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kv_dim = a.n_kv * HD;
+    const int pos_new = seq - 1;
+    const int w0 = c0 + wave * C::PW;  // this wave's first position
+    const bool live = w0 < seq;        // (wave-uniform, like w_new)
+    const bool w_new = FUSED && pos_new >= w0 && pos_new < w0 + C::PW;
+    unsigned char *kc = reinterpret_cast<unsigned char *>(a.k_cache);
+    unsigned char *vc = reinterpret_cast<unsigned char *>(a.v_cache);
+    const size_t row_bytes = (size_t)kv_dim * 2;
+    const int lg = lane >> 4, li = lane & 15;  // lane group, lane in group
+
+    // ---- 1. loads, straight-line (see attn_wave_kernel), in the order they
+    // are used: a query head (waves below HPK), the new k and v (the wave
+    // holding pos_new), the K rows in the MFMA A layout (key li, bytes
+    // 64 lg + 16 t), then the V rows in their natural layout (rows 4 i + lg,
+    // 16-byte unit li); rows past the sequence clamp to its last row ----
+    const int h = g * HPK + (wave < HPK ? wave : HPK - 1);
+    const bool q_wave = wave < HPK;
+    auto rs = [](const float *p, bool use) {
+        return make_rsrc(p, use ? (uint32_t)(HD * sizeof(float)) : 0u);
+    };
+    auto ld2 = [&](__amdgpu_buffer_rsrc_t r, float &x0, float &x1) {
+        x0 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, lane * 4, 0, 0));
+        x1 = __builtin_bit_cast(float,
+                                __builtin_amdgcn_raw_buffer_load_b32(r, (lane + HALF) * 4, 0, 0));
+    };
+    float lo, hi, gl = 0.f, gh = 0.f, cs = 0.f, sn = 0.f;
+    float klo = 0.f, khi = 0.f, kgl = 0.f, kgh = 0.f, v0 = 0.f, v1 = 0.f;
+    if constexpr (FUSED) {
+        const int q_dim = a.n_heads * HD;
+        const float *ks = a.qkv + q_dim + g * HD;
+        ld2(rs(a.qkv + (size_t)h * HD, q_wave), lo, hi);
+        ld2(rs(a.q_norm_w, q_wave), gl, gh);
+        const __amdgpu_buffer_rsrc_t rc =
+            make_rsrc(a.cos_t + (size_t)pos_new * HALF, (q_wave || w_new) ? HALF * 4 : 0u);
+        const __amdgpu_buffer_rsrc_t rsn =
+            make_rsrc(a.sin_t + (size_t)pos_new * HALF, (q_wave || w_new) ? HALF * 4 : 0u);
+        cs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rc, lane * 4, 0, 0));
+        sn = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsn, lane * 4, 0, 0));
+        ld2(rs(ks, w_new), klo, khi);
+        ld2(rs(a.k_norm_w, w_new), kgl, kgh);
+        ld2(rs(ks + kv_dim, w_new), v0, v1);
+    } else {
+        ld2(rs(a.q + (size_t)h * HD, q_wave), lo, hi);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 kr[4], vr[4];
+    {
+        int p = w0 + li;
+        p = p < seq ? p : seq - 1;
+        const unsigned char *src = kc + (size_t)p * row_bytes + (size_t)g * C::ROWB + lg * 64;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) kr[t] = *reinterpret_cast<const uint4 *>(src + 16 * t);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int p = w0 + 4 * i + lg;
+        p = p < seq ? p : seq - 1;
+        vr[i] = *reinterpret_cast<const uint4 *>(vc + (size_t)p * row_bytes +
+                                                (size_t)g * C::ROWB + (size_t)li * 16);
+    }
+
+    // ---- 2. query head of waves below HPK (normalised + rotated when
+    // fused), into LDS as f16 hi and lo parts ----
+    if (q_wave) {
+        float r0 = lo, r1 = hi;
+        if constexpr (FUSED) {
+            const float ss = wave_sum(lo * lo + hi * hi);
+            const float inv = 1.0f / sqrtf(ss / (float)HD + a.eps);
+            const float l0 = (lo * inv) * gl;
+            const float h0 = (hi * inv) * gh;
+            r0 = l0 * cs - h0 * sn;
+            r1 = h0 * cs + l0 * sn;
+            if (a.q_tap && c == 0) {  // the "q" tap (qwen3.rs:165)
+                a.q_tap[(size_t)h * HD + lane] = r0;
+                a.q_tap[(size_t)h * HD + lane + HALF] = r1;
+            }
+        }
+        const _Float16 a0 = (_Float16)r0, a1 = (_Float16)r1;
+        q16[wave * HD + lane] = a0;
+        q16[wave * HD + lane + HALF] = a1;
+        q16[(HPK + wave) * HD + lane] = (_Float16)(r0 - (float)a0);
+        q16[(HPK + wave) * HD + lane + HALF] = (_Float16)(r1 - (float)a1);
+    }
+
+    // ---- 3. the new position's k (normalised + rotated) and v: to the cache
+    // and to LDS, from where the lanes holding that row take them ----
+    if (w_new) {
+        const float kss = wave_sum(klo * klo + khi * khi);
+        const float kinv = 1.0f / sqrtf(kss / (float)HD + a.eps);
+        const float l0 = (klo * kinv) * kgl;
+        const float h0 = (khi * kinv) * kgh;
+        const _Float16 k0 = (_Float16)(l0 * cs - h0 * sn), k1 = (_Float16)(h0 * cs + l0 * sn);
+        const _Float16 vv0 = (_Float16)v0, vv1 = (_Float16)v1;
+        _Float16 *kg = reinterpret_cast<_Float16 *>(kc + (size_t)pos_new * row_bytes + (size_t)g * C::ROWB);
+        _Float16 *vg = reinterpret_cast<_Float16 *>(vc + (size_t)pos_new * row_bytes + (size_t)g * C::ROWB);
+        kg[lane] = k0;
+        kg[lane + HALF] = k1;
+        vg[lane] = vv0;
+        vg[lane + HALF] = vv1;
+        new_s[lane] = (float)k0;
+        new_s[lane + HALF] = (float)k1;
+        new_s[HD + lane] = (float)vv0;
+        new_s[HD + lane + HALF] = (float)vv1;
+    }
+    lds_barrier();  // q (and the new row) are in LDS
+    if (w_new) {
+        const int r = pos_new - w0;
+        if (li == r) {  // K in the A layout: this lane holds key r, dims 32 lg + 8 t ..
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                float kn[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) kn[e] = new_s[32 * lg + 8 * t + e];
+                kr[t] = pack16<_Float16>(kn);
+            }
+        }
+        float vn[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vn[e] = new_s[HD + li * 8 + e];
+        const uint4 vp = pack16<_Float16>(vn);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const bool mine = 4 * i + lg == r;
+            vr[i].x = mine ? vp.x : vr[i].x;
+            vr[i].y = mine ? vp.y : vr[i].y;
+            vr[i].z = mine ? vp.z : vr[i].z;
+            vr[i].w = mine ? vp.w : vr[i].w;
+        }
+    }
+
+    // od[t][r]: o of head 4 lg + r at dim 8 li + t (lane groups past the
+    // heads hold zeros)
+    f32x4 od[8];
+    float m[HPK], l[HPK];
+    if (live) {
+        // ---- 4. scores S^T[key 4 lg + r][head li] ----
+        f16x8 qb[4][2];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int part = 0; part < 2; ++part) {
+                f16x8 z = {};
+                if (li < HPK)
+                    z = *reinterpret_cast<const f16x8 *>(q16 + (part * HPK + li) * HD + 32 * lg + 8 * t);
+                qb[t][part] = z;
+            }
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const f16x8 ka = __builtin_bit_cast(f16x8, kr[t]);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[t][0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[t][1], acc, 0, 0, 0);
+        }
+
+        // ---- 5. softmax partial per head (lanes li < HPK hold head li's
+        // column: keys 4 lg + r) ----
+        float sv[4], mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const bool in = w0 + 4 * lg + r < seq;
+            sv[r] = in ? acc[r] * scale : -INFINITY;
+            mx = fmaxf(mx, sv[r]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        float ls = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            sv[r] = sv[r] == -INFINITY ? 0.0f : expf(sv[r] - mx);
+            ls += sv[r];
+        }
+        ls += __shfl_xor(ls, 16);
+        ls += __shfl_xor(ls, 32);
+        float *pw = p_all + wave * (C::PW * HPK);  // [key][head]
+        if (li < HPK) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pw[(4 * lg + r) * HPK + li] = sv[r];
+        }
+        // every lane needs (m, l) of every head: lane hh of group 0 holds head hh
+#pragma unroll
+        for (int hh = 0; hh < HPK; ++hh) {
+            m[hh] = __shfl(mx, hh);
+            l[hh] = __shfl(ls, hh);
+        }
+        wave_lds_sync();
+
+        // ---- 6. P.V on v_mfma_f32_16x16x16_f16 (lane l holds A[l % 16][4 (l / 16)
+        // + j], B[4 (l / 16) + j][l % 16], receives D[4 (l / 16) + r][l % 16]).
+        // The key order of k slot 4 lg + j is key 4 j + lg, which is V row j of
+        // this lane; output column li of MFMA t is dim 8 li + t, element t of
+        // this lane's unit.  So B comes straight from the V registers, A is p
+        // of head li (f16 hi + lo), and lanes 0..15 receive o[head r][dim
+        // 8 li + t]: the sum over all 16 keys, with no cross-lane reduction ----
+        f16x4 pa[2];
+        {
+            float pv[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) pv[j] = li < HPK ? pw[(4 * j + lg) * HPK + li] : 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const _Float16 hi16 = (_Float16)pv[j];
+                pa[0][j] = hi16;
+                pa[1][j] = (_Float16)(pv[j] - (float)hi16);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            f16x4 vb;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) vb[j] = __builtin_bit_cast(f16x8, vr[j])[t];
+            f32x4 z = {0.f, 0.f, 0.f, 0.f};
+            z = __builtin_amdgcn_mfma_f32_16x16x16f16(pa[0], vb, z, 0, 0, 0);
+            od[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa[1], vb, z, 0, 0, 0);
+        }
+    } else {
+#pragma unroll
+        for (int hh = 0; hh < HPK; ++hh) {
+            m[hh] = -INFINITY;
+            l[hh] = 0.0f;
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) od[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // ---- 7. the wave's partial (o, m, l) per head into LDS: lane group lg
+    // holds heads 4 lg .. 4 lg + 3 ----
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int hh = 4 * lg + r;
+        if (hh < HPK) {
+            float *dst = wp + (wave * HPK + hh) * (HD + 2);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) dst[8 * li + t] = od[t][r];
+        }
+    }
+    if (lane < HPK) {
+        float *dst = wp + (wave * HPK + lane) * (HD + 2);
+        float mm = m[0], ll = l[0];
+#pragma unroll
+        for (int hh = 1; hh < HPK; ++hh) {
+            mm = lane == hh ? m[hh] : mm;
+            ll = lane == hh ? l[hh] : ll;
+        }
+        dst[HD] = mm;
+        dst[HD + 1] = ll;
+    }
+    __syncthreads();
+
+    // ---- 8. merge of the W wave partials: the W x HPK weights exp(m_w - M)
+    // once (one lane each, into the p tiles' space), then thread -> (head,
+    // dim) sums; the chunk partial goes to memory write-through, or the
+    // output for one chunk ----
+    float *fac = p_all;             // [W][HPK] weights
+    float *fl = p_all + W * HPK;    // [W][HPK] weight * l
+    if (tid < W * HPK) {
+        const int w = tid / HPK, hh = tid % HPK;
+        float M = -INFINITY;
+        for (int v = 0; v < W; ++v) M = fmaxf(M, wp[(v * HPK + hh) * (HD + 2) + HD]);
+        const float *src = wp + (w * HPK + hh) * (HD + 2);
+        const float f = src[HD] == -INFINITY ? 0.0f : expf(src[HD] - M);
+        fac[tid] = f;
+        fl[tid] = f * src[HD + 1];
+    }
+    __syncthreads();
+    float *const part_ml = a.part + (size_t)a.n_heads * max_chunks * HD;
+    for (int idx = tid; idx < HPK * HD; idx += (int)blockDim.x) {
+        const int hh = idx / HD, d = idx % HD;
+        float O = 0.0f;
+        for (int w = 0; w < W; ++w)
+            O = __builtin_fmaf(fac[w * HPK + hh], wp[(w * HPK + hh) * (HD + 2) + d], O);
+        const int hg = g * HPK + hh;
+        if (n_chunks == 1) {
+            float L = 0.0f;
+            for (int w = 0; w < W; ++w) L += fl[w * HPK + hh];
+            a.out[(size_t)hg * HD + d] = O / L;
+        } else {
+            st_part(a.part + ((size_t)hg * max_chunks + c) * HD + d, O);
+            if (d == 0) {
+                float M = -INFINITY, L = 0.0f;
+                for (int w = 0; w < W; ++w) {
+                    M = fmaxf(M, wp[(w * HPK + hh) * (HD + 2) + HD]);
+                    L += fl[w * HPK + hh];
+                }
+                float *pml = part_ml + ((size_t)hg * max_chunks + c) * 2;
+                st_part(pml, M);
+                st_part(pml + 1, L);
+            }
+        }
+    }
+    if (n_chunks == 1) return;
+
+    // ---- 9. arrival, then the last arriver merges the chunks ----
+    __shared__ int last_s;
+    drain();
+    __syncthreads();
+    if (tid == 0) {
+        unsigned *cnt = a.cnt + 32 * g;
+        const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = old + 1 == (unsigned)n_chunks;
+        if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_s = last;
+    }
+    __syncthreads();
+    if (!last_s) return;
+    if (wave < HPK)
+        merge_chunks<HD, C::MAXC>(a, g * HPK + wave, n_chunks, max_chunks, wp + wave * C::MAXC,
+                                  lane);
 }
 
 typedef void (*attn_fn)(cwi::AttnArgs, float, int);
@@ -676,20 +1478,96 @@ AttnPick pick_attn(int kv_dtype, int hd, int hpk) {
     return kv_dtype == CW_F16 ? pick_hd<_Float16>(hd, hpk) : pick_hd<float>(hd, hpk);
 }
 
+template <typename KVT, int HPK, int W>
+AttnPick make_wave_pick(bool fused) {
+    using C = WaveCfg<KVT, HPK, W>;
+    return {fused ? attn_wave_kernel<KVT, HPK, W, true> : attn_wave_kernel<KVT, HPK, W, false>,
+            C::THREADS, C::CP, C::LDS};
+}
+
+template <typename KVT>
+AttnPick pick_wave_w(int hpk, int w, bool f) {
+    switch (hpk) {
+        case 1: return w == 8 ? make_wave_pick<KVT, 1, 8>(f)
+                       : w == 4 ? make_wave_pick<KVT, 1, 4>(f) : make_wave_pick<KVT, 1, 2>(f);
+        case 2: return w == 8 ? make_wave_pick<KVT, 2, 8>(f)
+                       : w == 4 ? make_wave_pick<KVT, 2, 4>(f) : make_wave_pick<KVT, 2, 2>(f);
+        case 4: return w == 8 ? make_wave_pick<KVT, 4, 8>(f) : make_wave_pick<KVT, 4, 4>(f);
+        case 8: return make_wave_pick<KVT, 8, 8>(f);
+        default: return {nullptr, 0, 0, 0};
+    }
+}
+
+// head_dim 128: the register-resident kernel, with W waves (16 positions
+// each) per workgroup: the largest W (at least the heads per kv head) whose
+// grid for a full cache still gives every CU a workgroup, else the smallest
+AttnPick pick_wave(const cw_ctx *ctx, int kv_dtype, int hpk, int n_kv, int max_seq, bool fused) {
+    int w = 2;
+    for (int cand : {8, 4, 2}) {
+        if (cand < hpk) continue;
+        w = cand;
+        const long wgs = (long)((max_seq + 16 * cand - 1) / (16 * cand)) * n_kv;
+        if (wgs >= ctx->n_cu) break;
+    }
+    if (w < hpk) w = hpk;
+    return kv_dtype == CW_F16 ? pick_wave_w<_Float16>(hpk, w, fused)
+                              : pick_wave_w<float>(hpk, w, fused);
+}
+
 }  // namespace
 
 namespace cwi {
 
 size_t attn_scratch_floats(int n_heads, int n_kv, int hd, int max_seq) {
-    const AttnPick pk = pick_attn(CW_F32, hd, n_heads / n_kv);  // f32: smallest chunk
-    const int cp = pk.cp > 0 ? pk.cp : 8;
+    // chunks of at least 16 positions (the head_dim-128 kernel's smallest;
+    // the general kernel's are no smaller for these shapes)
+    const AttnPick pk = pick_attn(CW_F32, hd, n_heads / n_kv);
+    int cp = pk.cp > 0 ? pk.cp : 8;
+    if (cp > 16) cp = 16;
     const size_t chunks = (size_t)(max_seq + cp - 1) / cp;
     return chunks * (size_t)n_heads * (hd + 2);
 }
 
+// f16 cache, head_dim 128: the MFMA kernel with W waves (16 positions each)
+// per workgroup, the fewest that keep a full cache's grid within one
+// workgroup per CU (at least HPK waves, at most 16)
+template <int HPK>
+int launch_mfma_hpk(cw_ctx *ctx, const AttnArgs &b, float scale) {
+    using C = MfmaCfg<HPK>;
+    const long per_cu = ((long)b.max_seq * b.n_kv + ctx->n_cu - 1) / ctx->n_cu;
+    int w = (int)((per_cu + C::PW - 1) / C::PW);
+    w = w < HPK ? HPK : w > C::WMAX ? C::WMAX : w;
+    const int max_chunks = (b.max_seq + C::PW * w - 1) / (C::PW * w);
+    auto fn = b.qkv ? attn_mfma_kernel<HPK, true> : attn_mfma_kernel<HPK, false>;
+    CW_TRY(ensure_lds(fn, C::LDS));
+    return launch(ctx, "attention", fn, dim3(max_chunks, b.n_kv), dim3(64 * w), C::LDS, b, scale,
+                  max_chunks);
+}
+
 int launch_attention(cw_ctx *ctx, const AttnArgs &a) {
     const int hpk = a.n_heads / a.n_kv;
-    const AttnPick pk = pick_attn(a.kv_dtype, a.hd, hpk);
+    if (a.hd == 128 && a.kv_dtype == CW_F16) {
+        if (a.max_seq > kMaxChunkSpan) {
+            set_error("attention: max_seq=%d exceeds %d", a.max_seq, kMaxChunkSpan);
+            return CW_ERR_ARG;
+        }
+        if (a.n_kv > kMaxAttnKv) {
+            set_error("attention: n_kv_heads=%d exceeds %d", a.n_kv, kMaxAttnKv);
+            return CW_ERR_ARG;
+        }
+        AttnArgs b = a;
+        b.cnt = ctx->attn_cnt;
+        const float scale = powf((float)a.hd, -0.5f);
+        switch (hpk) {
+            case 1: return launch_mfma_hpk<1>(ctx, b, scale);
+            case 2: return launch_mfma_hpk<2>(ctx, b, scale);
+            case 4: return launch_mfma_hpk<4>(ctx, b, scale);
+            case 8: return launch_mfma_hpk<8>(ctx, b, scale);
+            default: break;
+        }
+    }
+    const AttnPick pk = a.hd == 128 ? pick_wave(ctx, a.kv_dtype, hpk, a.n_kv, a.max_seq, a.qkv != nullptr)
+                                    : pick_attn(a.kv_dtype, a.hd, hpk);
     if (!pk.fn) {
         set_error("attention: unsupported head_dim=%d / heads per kv=%d", a.hd, hpk);
         return CW_ERR_ARG;
@@ -707,11 +1585,8 @@ int launch_attention(cw_ctx *ctx, const AttnArgs &a) {
     AttnArgs b = a;
     b.cnt = ctx->attn_cnt;
     const float scale = powf((float)a.hd, -0.5f);
-    prof_begin(ctx, "attention");
-    hipLaunchKernelGGL(pk.fn, dim3(max_chunks, a.n_kv), dim3(pk.threads), pk.lds, ctx->stream, b,
-                       scale, max_chunks);
-    prof_end(ctx);
-    return launch_check("attention");
+    return launch(ctx, "attention", pk.fn, dim3(max_chunks, a.n_kv), dim3(pk.threads), pk.lds, b,
+                  scale, max_chunks);
 }
 
 }  // namespace cwi
