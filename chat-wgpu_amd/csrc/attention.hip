@@ -1461,18 +1461,34 @@ AttnPick pick_hd(int hd, int hpk) {
     }
 }
 
+// Kernels whose LDS limit was raised already: a fixed table (no heap
+// allocation on the launch path, which cw_attention_noalloc relies on)
 std::mutex g_mu;
-std::map<const void *, bool> g_lds_set;
+constexpr int kLdsSlots = 128;
+const void *g_lds_set[kLdsSlots];
+int g_lds_n = 0;
 
 int ensure_lds(attn_fn f, int lds) {
     std::lock_guard<std::mutex> lk(g_mu);
     const void *p = reinterpret_cast<const void *>(f);
-    if (!g_lds_set[p]) {
-        CW_HIP(hipFuncSetAttribute(p, hipFuncAttributeMaxDynamicSharedMemorySize, lds));
-        g_lds_set[p] = true;
-    }
+    for (int i = 0; i < g_lds_n; ++i)
+        if (g_lds_set[i] == p) return CW_OK;
+    CW_HIP(hipFuncSetAttribute(p, hipFuncAttributeMaxDynamicSharedMemorySize, lds));
+    if (g_lds_n < kLdsSlots) g_lds_set[g_lds_n++] = p;
     return CW_OK;
 }
+
+// ---- the scratch of cw_attention_noalloc: chunk partials, then the
+// per-kv-head arrival counters (one 128-byte line each).  One copy per GPU,
+// shared by every call on that GPU; its address is taken once per device
+// (attn_noalloc_setup, from cw_ctx_create).
+constexpr size_t kNoAllocPartBytes = (size_t)8 << 20;
+constexpr size_t kNoAllocCntBytes = (size_t)cwi::kMaxAttnKv * 128;
+static __device__ __align__(256) unsigned char scratch[kNoAllocPartBytes + kNoAllocCntBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+void *g_noalloc_ptr[kMaxDevices];
 
 AttnPick pick_attn(int kv_dtype, int hd, int hpk) {
     return kv_dtype == CW_F16 ? pick_hd<_Float16>(hd, hpk) : pick_hd<float>(hd, hpk);
@@ -1532,7 +1548,7 @@ size_t attn_scratch_floats(int n_heads, int n_kv, int hd, int max_seq) {
 // per workgroup, the fewest that keep a full cache's grid within one
 // workgroup per CU (at least HPK waves, at most 16)
 template <int HPK>
-int launch_mfma_hpk(cw_ctx *ctx, const AttnArgs &b, float scale) {
+int launch_mfma_hpk(cw_ctx *ctx, const AttnArgs &b, float scale, bool prof) {
     using C = MfmaCfg<HPK>;
     const long per_cu = ((long)b.max_seq * b.n_kv + ctx->n_cu - 1) / ctx->n_cu;
     int w = (int)((per_cu + C::PW - 1) / C::PW);
@@ -1540,11 +1556,22 @@ int launch_mfma_hpk(cw_ctx *ctx, const AttnArgs &b, float scale) {
     const int max_chunks = (b.max_seq + C::PW * w - 1) / (C::PW * w);
     auto fn = b.qkv ? attn_mfma_kernel<HPK, true> : attn_mfma_kernel<HPK, false>;
     CW_TRY(ensure_lds(fn, C::LDS));
+    if (!prof) {
+        hipLaunchKernelGGL(fn, dim3(max_chunks, b.n_kv), dim3(64 * w), C::LDS, ctx->stream, b,
+                           scale, max_chunks);
+        return launch_check("attention");
+    }
     return launch(ctx, "attention", fn, dim3(max_chunks, b.n_kv), dim3(64 * w), C::LDS, b, scale,
                   max_chunks);
 }
 
-int launch_attention(cw_ctx *ctx, const AttnArgs &a) {
+// Enqueue attention; a.cnt (the arrival counters) defaults to the context's.
+// Without `prof` no profiling events are taken (their creation allocates).
+int launch_attention_impl(cw_ctx *ctx, const AttnArgs &a, bool prof);
+
+int launch_attention(cw_ctx *ctx, const AttnArgs &a) { return launch_attention_impl(ctx, a, true); }
+
+int launch_attention_impl(cw_ctx *ctx, const AttnArgs &a, bool prof) {
     const int hpk = a.n_heads / a.n_kv;
     if (a.hd == 128 && a.kv_dtype == CW_F16) {
         if (a.max_seq > kMaxChunkSpan) {
@@ -1556,13 +1583,13 @@ int launch_attention(cw_ctx *ctx, const AttnArgs &a) {
             return CW_ERR_ARG;
         }
         AttnArgs b = a;
-        b.cnt = ctx->attn_cnt;
+        b.cnt = a.cnt ? a.cnt : ctx->attn_cnt;
         const float scale = powf((float)a.hd, -0.5f);
         switch (hpk) {
-            case 1: return launch_mfma_hpk<1>(ctx, b, scale);
-            case 2: return launch_mfma_hpk<2>(ctx, b, scale);
-            case 4: return launch_mfma_hpk<4>(ctx, b, scale);
-            case 8: return launch_mfma_hpk<8>(ctx, b, scale);
+            case 1: return launch_mfma_hpk<1>(ctx, b, scale, prof);
+            case 2: return launch_mfma_hpk<2>(ctx, b, scale, prof);
+            case 4: return launch_mfma_hpk<4>(ctx, b, scale, prof);
+            case 8: return launch_mfma_hpk<8>(ctx, b, scale, prof);
             default: break;
         }
     }
@@ -1583,30 +1610,96 @@ int launch_attention(cw_ctx *ctx, const AttnArgs &a) {
     CW_TRY(ensure_lds(pk.fn, pk.lds));
     const int max_chunks = (a.max_seq + pk.cp - 1) / pk.cp;
     AttnArgs b = a;
-    b.cnt = ctx->attn_cnt;
+    b.cnt = a.cnt ? a.cnt : ctx->attn_cnt;
     const float scale = powf((float)a.hd, -0.5f);
+    if (!prof) {
+        hipLaunchKernelGGL(pk.fn, dim3(max_chunks, a.n_kv), dim3(pk.threads), pk.lds, ctx->stream,
+                           b, scale, max_chunks);
+        return launch_check("attention");
+    }
     return launch(ctx, "attention", pk.fn, dim3(max_chunks, a.n_kv), dim3(pk.threads), pk.lds, b,
                   scale, max_chunks);
+}
+
+int attn_noalloc_setup(cw_ctx *ctx) {
+    CW_CHECK_ARG(ctx->device >= 0 && ctx->device < kMaxDevices,
+                 "attention scratch: device %d beyond %d", ctx->device, kMaxDevices);
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (!g_noalloc_ptr[ctx->device]) {
+        // this device's copy of the array (the caller made the device current);
+        // the counters must start at zero, every launch leaves them at zero
+        void *ptr = nullptr;
+        CW_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        CW_HIP(hipMemsetAsync(static_cast<unsigned char *>(ptr) + kNoAllocPartBytes, 0,
+                              kNoAllocCntBytes, ctx->stream));
+        CW_HIP(hipStreamSynchronize(ctx->stream));
+        g_noalloc_ptr[ctx->device] = ptr;
+    }
+    ctx->noalloc_scratch = g_noalloc_ptr[ctx->device];
+    return CW_OK;
 }
 
 }  // namespace cwi
 
 using namespace cwi;
 
-extern "C" int cw_attention(cw_ctx *ctx, const float *q, const void *k, const void *v, int kv_dtype,
-                            int n_heads, int n_kv_heads, int seq, int head_dim, float *out) {
-    CW_CHECK_ARG(ctx && q && k && v && out, "cw_attention: null argument");
-    CW_CHECK_ARG(kv_dtype == CW_F32 || kv_dtype == CW_F16, "cw_attention: kv_dtype=%d", kv_dtype);
+static int check_attention_args(const char *what, const float *q, const void *k, const void *v,
+                                int kv_dtype, int n_heads, int n_kv_heads, int seq, int head_dim,
+                                const float *out) {
+    CW_CHECK_ARG(q && k && v && out, "%s: null argument", what);
+    CW_CHECK_ARG(kv_dtype == CW_F32 || kv_dtype == CW_F16, "%s: kv_dtype=%d", what, kv_dtype);
     CW_CHECK_ARG(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0,
-                 "cw_attention: n_heads=%d n_kv_heads=%d", n_heads, n_kv_heads);
-    CW_CHECK_ARG(seq > 0 && seq <= kMaxChunkSpan, "cw_attention: seq=%d outside [1, %d]", seq,
+                 "%s: n_heads=%d n_kv_heads=%d", what, n_heads, n_kv_heads);
+    CW_CHECK_ARG(seq > 0 && seq <= kMaxChunkSpan, "%s: seq=%d outside [1, %d]", what, seq,
                  kMaxChunkSpan);
     const int hpk = n_heads / n_kv_heads;
     CW_CHECK_ARG(hpk == 1 || hpk == 2 || hpk == 4 || hpk == 8,
-                 "cw_attention: heads per kv head %d not in {1,2,4,8}", hpk);
+                 "%s: heads per kv head %d not in {1,2,4,8}", what, hpk);
     CW_CHECK_ARG(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128 ||
                      head_dim == 256,
-                 "cw_attention: head_dim=%d not in {16,32,64,128,256}", head_dim);
+                 "%s: head_dim=%d not in {16,32,64,128,256}", what, head_dim);
+    return CW_OK;
+}
+
+extern "C" int cw_attention_noalloc(cw_ctx *ctx, const float *q, const void *k, const void *v,
+                                    int kv_dtype, int n_heads, int n_kv_heads, int seq,
+                                    int head_dim, float *out) {
+    CW_CHECK_ARG(ctx != nullptr, "cw_attention_noalloc: null ctx");
+    CW_TRY(check_attention_args("cw_attention_noalloc", q, k, v, kv_dtype, n_heads, n_kv_heads,
+                                seq, head_dim, out));
+    CW_CHECK_ARG(n_kv_heads <= kMaxAttnKv, "cw_attention_noalloc: n_kv_heads=%d exceeds %d",
+                 n_kv_heads, kMaxAttnKv);
+    const size_t need = attn_scratch_floats(n_heads, n_kv_heads, head_dim, seq) * sizeof(float);
+    CW_CHECK_ARG(need <= kNoAllocPartBytes,
+                 "cw_attention_noalloc: the chunk partials need %zu bytes, the static scratch "
+                 "holds %zu (n_heads * ceil(seq / 16) * (head_dim + 2) floats)",
+                 need, kNoAllocPartBytes);
+    if (!ctx->noalloc_scratch) {
+        set_error("cw_attention_noalloc: the context has no static scratch address");
+        return CW_ERR_STATE;
+    }
+    AttnArgs a{};
+    a.q = q;
+    a.k_cache = const_cast<void *>(k);
+    a.v_cache = const_cast<void *>(v);
+    a.kv_dtype = kv_dtype;
+    a.n_heads = n_heads;
+    a.n_kv = n_kv_heads;
+    a.hd = head_dim;
+    a.seq = seq;
+    a.max_seq = seq;
+    a.out = out;
+    unsigned char *base = static_cast<unsigned char *>(ctx->noalloc_scratch);
+    a.part = reinterpret_cast<float *>(base);
+    a.cnt = reinterpret_cast<unsigned *>(base + kNoAllocPartBytes);
+    return launch_attention_impl(ctx, a, false);
+}
+
+extern "C" int cw_attention(cw_ctx *ctx, const float *q, const void *k, const void *v, int kv_dtype,
+                            int n_heads, int n_kv_heads, int seq, int head_dim, float *out) {
+    CW_CHECK_ARG(ctx != nullptr, "cw_attention: null argument");
+    CW_TRY(check_attention_args("cw_attention", q, k, v, kv_dtype, n_heads, n_kv_heads, seq,
+                                head_dim, out));
     const size_t nfl = attn_scratch_floats(n_heads, n_kv_heads, head_dim, seq);
     void *scratch = nullptr;
     CW_TRY(ctx_scratch(ctx, nfl * sizeof(float), &scratch));

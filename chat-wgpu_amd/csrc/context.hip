@@ -231,6 +231,11 @@ int cw_ctx_create(int device, cw_ctx **out) {
         delete ctx;
         return hip_fail(e, "attention counters", __FILE__, __LINE__);
     }
+    const int rc = cwi::attn_noalloc_setup(ctx);
+    if (rc != CW_OK) {
+        cw_ctx_destroy(ctx);
+        return rc;
+    }
     *out = ctx;
     return CW_OK;
 }

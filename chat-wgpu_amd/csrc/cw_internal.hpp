@@ -108,6 +108,9 @@ struct cw_ctx {
     // sequence may still name them, so they live until cw_ctx_destroy
     std::vector<void *> scratch_retired;
 
+    // this device's static scratch of cw_attention_noalloc (set at create)
+    void *noalloc_scratch = nullptr;
+
     // RoPE tables; a deque, so a table's address stays valid as others are added
     std::deque<cw_rope_tab> ropes;
 
@@ -211,6 +214,9 @@ struct AttnArgs {
 constexpr int kMaxAttnKv = 1024;
 
 size_t attn_scratch_floats(int n_heads, int n_kv, int hd, int max_seq);
+// Take this device's address of cw_attention_noalloc's static scratch (once
+// per device; the device must be current) and clear its counters.
+int attn_noalloc_setup(cw_ctx *ctx);
 int launch_attention(cw_ctx *ctx, const AttnArgs &a);
 
 int launch_rmsnorm(cw_ctx *ctx, const float *x, const float *w, int rows, int dim, float eps,

@@ -82,6 +82,7 @@ _SIGS = {
     "cw_rmsnorm": (_I, [_P, _P, _P, _I, _I, _F, _P]),
     "cw_rope": (_I, [_P, _P, _I, _I, _I, _F, _P]),
     "cw_attention": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "cw_attention_noalloc": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "cw_add": (_I, [_P, _P, _P, _I, _P]),
     "cw_swiglu": (_I, [_P, _P, _P, _I, _P]),
     "cw_argmax": (_I, [_P, _P, _I, _P]),

@@ -127,6 +127,19 @@ int cw_rope(cw_ctx *ctx, const float *x, int rows, int head_dim, int pos, float 
  * element type kv_dtype (CW_F32 or CW_F16).  head_dim in {16,32,64,128,256}. */
 int cw_attention(cw_ctx *ctx, const float *q, const void *k, const void *v, int kv_dtype,
                  int n_heads, int n_kv_heads, int seq, int head_dim, float *out);
+/* No counterpart in the reference: cw_attention for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments and results as cw_attention, but the
+ * chunk partials and arrival counters live in a static device array of
+ * 8 MiB + 128 KiB that each GPU holds from the first cw_ctx_create on it
+ * until the process ends; the call allocates nothing (no device memory, no
+ * profiling events).  Limit: n_heads * ceil(seq / 16) * (head_dim + 2) * 4
+ * bytes of partials must fit 8 MiB (32 heads of 128 dims: seq <= 8064), else
+ * CW_ERR_ARG.  Every call on a GPU shares that GPU's array, so calls that
+ * overlap on one GPU (other streams, other contexts) race. */
+int cw_attention_noalloc(cw_ctx *ctx, const float *q, const void *k, const void *v,
+                         int kv_dtype, int n_heads, int n_kv_heads, int seq, int head_dim,
+                         float *out);
 /* attention::add (src/kernels/attention.rs:40-51, ewise.wgsl:9-13): c = a + b. */
 int cw_add(cw_ctx *ctx, const float *a, const float *b, int n, float *c);
 /* activation::swiglu (src/kernels/activation.rs:42-44, glu.wgsl:22-26). */
