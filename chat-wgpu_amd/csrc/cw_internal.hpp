@@ -172,7 +172,12 @@ float f16_bits_to_f32(uint16_t h);
 // ---- kernel launchers (all enqueue on ctx->stream) ----
 
 enum XSrc { XS_PLAIN = 0, XS_RMSNORM = 1 };
-enum Epi { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2 };
+// EPI_ARGMAX: store, and the argmax of y over the whole launch (the last
+// workgroup to finish merges the workgroups' bests and advances the decode
+// state, like launch_argmax)
+enum Epi { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3 };
+
+struct GenState;
 
 struct GemvArgs {
     const float *x;         // activation [K] (raw hidden for XS_RMSNORM)
@@ -185,6 +190,21 @@ struct GemvArgs {
     const float *resid;     // EPI_ADD
     float *y;               // [N]
     int K, N;
+    // x (resid) as row x_tok[0] (resid_tok[0]) of a table of tok_rows rows
+    // at that pointer, when set: the embedding row of the device-resident
+    // token (Qwen3::embed, qwen3.rs:128-133), read by the first layer
+    const uint32_t *x_tok;
+    const uint32_t *resid_tok;
+    int tok_rows;
+    // EPI_ARGMAX: per-workgroup bests [grid], the arrival counter (zero
+    // between launches), the argmax output and the generate state to advance
+    float *am_v;
+    uint32_t *am_i;
+    unsigned *am_cnt;
+    uint32_t *am_out;
+    GenState *state;
+    const uint32_t *prompt;
+    uint32_t *tokens;
 };
 
 int launch_q4_gemv(cw_ctx *ctx, XSrc xs, Epi epi, const GemvArgs &a);
@@ -241,6 +261,12 @@ struct GenState {
     int max_out;
 };
 size_t argmax_scratch_bytes(int n);
+// Scratch of the LM head's fused argmax (EPI_ARGMAX): per-workgroup bests
+// for any grid launch_q4_gemv picks, then the arrival counter line.
+size_t lm_argmax_scratch_bytes(const cw_ctx *ctx);
+// The LM head with the fused argmax over its own scratch (zeroed once).
+int launch_lm_head_argmax(cw_ctx *ctx, GemvArgs g, void *scratch, uint32_t *out_dev,
+                          GenState *state, const uint32_t *prompt_dev, uint32_t *tokens_out_dev);
 int launch_argmax(cw_ctx *ctx, const float *logits, int n, uint32_t *out_dev, void *scratch,
                   GenState *state, const uint32_t *prompt_dev, uint32_t *tokens_out_dev);
 

@@ -69,6 +69,7 @@ struct cw_model {
     float *tap_q = nullptr, *tap_post = nullptr, *tap_out = nullptr;
     float *part = nullptr;
     void *argmax_scratch = nullptr;
+    void *lm_scratch = nullptr;  // the LM head's fused argmax (counter zero between launches)
     GenState *state = nullptr;
     uint32_t *prompt_dev = nullptr, *tokens_dev = nullptr, *argmax_out = nullptr;
     bool finalized = false;
@@ -203,14 +204,18 @@ float *last_hidden(cw_model *m) {
 int enqueue_step(cw_model *m) {
     cw_ctx *ctx = m->ctx;
     const auto &c = m->cfg;
-    CW_TRY(launch_embed(ctx, m->embed, c.vocab, c.dim, &m->state->token, m->hidden));
-    float *h_in = m->hidden;  // this layer's input; updated in place unless taps are on
+    // the first layer reads the token's embedding row itself (its QKV input
+    // and its attention residual): no separate gather launch
+    const float *h_in = m->hidden;  // this layer's input; updated in place unless taps are on
     for (int i = 0; i < c.n_layers; ++i) {
         Layer &L = m->layers[i];
-        float *h_post = m->taps ? m->tap_post + (size_t)i * c.dim : h_in;
+        float *h_post = m->taps ? m->tap_post + (size_t)i * c.dim : m->hidden;
         float *h_out = m->taps ? m->tap_out + (size_t)i * c.dim : h_post;
+        const bool first = i == 0;
         GemvArgs g{};
-        g.x = h_in;
+        g.x = first ? m->embed : h_in;
+        g.x_tok = first ? &m->state->token : nullptr;
+        g.tok_rows = c.vocab;
         g.norm_w = L.attn_norm;
         g.eps = c.eps;
         g.sA = L.qkv.s;
@@ -244,7 +249,9 @@ int enqueue_step(cw_model *m) {
         g.x = m->attn;
         g.sA = L.wo.s;
         g.qA = L.wo.q;
-        g.resid = h_in;
+        g.resid = first ? m->embed : h_in;
+        g.resid_tok = first ? &m->state->token : nullptr;
+        g.tok_rows = c.vocab;
         g.y = h_post;
         g.K = m->q_dim;
         g.N = c.dim;
@@ -283,10 +290,9 @@ int enqueue_step(cw_model *m) {
     g.y = m->logits;
     g.K = c.dim;
     g.N = c.vocab;
-    CW_TRY(launch_q4_gemv(ctx, XS_RMSNORM, EPI_STORE, g));
-    CW_TRY(launch_argmax(ctx, m->logits, c.vocab, m->argmax_out, m->argmax_scratch, m->state,
-                         m->prompt_dev, m->tokens_dev));
-    return CW_OK;
+    // logits, their argmax and the generate state's advance in one launch
+    return launch_lm_head_argmax(ctx, g, m->lm_scratch, m->argmax_out, m->state, m->prompt_dev,
+                                 m->tokens_dev);
 }
 
 int ensure_graph(cw_model *m) {
@@ -652,6 +658,8 @@ int model_alloc(cw_model *m, const cw_model_config &c) {
     CW_TRY(dalloc(m, (size_t)c.vocab * 4, (void **)&m->logits));
     CW_TRY(dalloc(m, part_floats * 4, (void **)&m->part));
     CW_TRY(dalloc(m, argmax_scratch_bytes(c.vocab), &m->argmax_scratch));
+    CW_TRY(dalloc(m, m->dry ? (size_t)4 * m->dry_n_cu * 8 + 256 : lm_argmax_scratch_bytes(m->ctx),
+                  &m->lm_scratch));
     CW_TRY(dalloc(m, sizeof(GenState), (void **)&m->state));
     CW_TRY(dalloc(m, (size_t)c.max_seq * 4, (void **)&m->prompt_dev));
     CW_TRY(dalloc(m, (size_t)c.max_seq * 4, (void **)&m->tokens_dev));
@@ -700,7 +708,8 @@ int cw_model_create(cw_ctx *ctx, const cw_model_config *cfg, cw_model **out) {
     // zero the caches so positions never written read as 0, not garbage
     // cleared on the context stream, so every later copy and launch is ordered after
     if (hipMemsetAsync(m->kcache, 0, m->kv_layer_bytes * c.n_layers, ctx->stream) != hipSuccess ||
-        hipMemsetAsync(m->vcache, 0, m->kv_layer_bytes * c.n_layers, ctx->stream) != hipSuccess) {
+        hipMemsetAsync(m->vcache, 0, m->kv_layer_bytes * c.n_layers, ctx->stream) != hipSuccess ||
+        hipMemsetAsync(m->lm_scratch, 0, lm_argmax_scratch_bytes(ctx), ctx->stream) != hipSuccess) {
         set_error("cw_model_create: clearing the KV cache failed");
         cw_model_destroy(m);
         return CW_ERR_HIP;
@@ -1078,9 +1087,8 @@ int cw_model_prefill(cw_model *m, const uint32_t *tokens, int n, int start_pos,
         g.y = m->logits;
         g.K = c.dim;
         g.N = c.vocab;
-        CW_TRY(launch_q4_gemv(m->ctx, XS_RMSNORM, EPI_STORE, g));
-        CW_TRY(launch_argmax(m->ctx, m->logits, c.vocab, m->argmax_out, m->argmax_scratch,
-                             nullptr, nullptr, nullptr));
+        CW_TRY(launch_lm_head_argmax(m->ctx, g, m->lm_scratch, m->argmax_out, nullptr, nullptr,
+                                     nullptr));
         CW_TRY(launch_rmsnorm(m->ctx, last, m->final_norm, 1, c.dim, c.eps, m->hidden_out));
     } else {
         // head_dim other than 128 or an f32 cache: the per-token step, n times

@@ -96,6 +96,89 @@ __device__ __forceinline__ float dot_word(uint32_t dw, float4 xl, float4 xh, flo
     return s;
 }
 
+// ---- argmax over the launch (argmax.wgsl:18-55): candidates need v above
+// kNegInit (strict, so NaN never wins), the lowest index among equal values
+struct Best {
+    float v;
+    uint32_t i;
+};
+constexpr float kNegInit = -3.402823e38f;
+
+__device__ __forceinline__ Best better(Best a, Best b) {
+    if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
+    return a;
+}
+
+__device__ __forceinline__ Best wave_best(Best b) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        Best o{__shfl_xor(b.v, off), (uint32_t)__shfl_xor((int)b.i, off)};
+        b = better(b, o);
+    }
+    return b;
+}
+
+// The workgroup's best goes to memory write-through (am_v/am_i[block]); its
+// stores are complete before one agent-scope increment of the counter; the
+// last workgroup to arrive reads every best with agent-scope loads, writes
+// the argmax and advances the generate state (mod.rs:114-122: feed
+// prompt[p+1] inside the prompt, else record the argmax and feed it back),
+// and resets the counter for the next launch.
+__device__ __forceinline__ void argmax_tail(const GemvArgs &a, Best best, int tid, int lane,
+                                          int wave) {
+    __shared__ float bv[kWaves];
+    __shared__ uint32_t bi[kWaves];
+    __shared__ int last_s;
+    best = wave_best(best);
+    if (lane == 0) {
+        bv[wave] = best.v;
+        bi[wave] = best.i;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        Best r{bv[0], bi[0]};
+        for (int w = 1; w < kWaves; ++w) r = better(r, Best{bv[w], bi[w]});
+        __hip_atomic_store(a.am_v + blockIdx.x, r.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.am_i + blockIdx.x, r.i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        const unsigned old = __hip_atomic_fetch_add(a.am_cnt, 1u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = old + 1 == gridDim.x;
+        if (last) __hip_atomic_store(a.am_cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_s = last;
+    }
+    __syncthreads();
+    if (!last_s) return;
+    Best b{kNegInit, 0u};
+    for (int i = tid; i < (int)gridDim.x; i += kThreads)
+        b = better(b, Best{__hip_atomic_load(a.am_v + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                           __hip_atomic_load(a.am_i + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)});
+    b = wave_best(b);
+    __syncthreads();  // every wave is done with bv / bi above
+    if (lane == 0) {
+        bv[wave] = b.v;
+        bi[wave] = b.i;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        Best r{bv[0], bi[0]};
+        for (int w = 1; w < kWaves; ++w) r = better(r, Best{bv[w], bi[w]});
+        if (a.am_out) *a.am_out = r.i;
+        cwi::GenState *st = a.state;
+        if (st) {
+            const int p = st->pos - st->start_pos;
+            if (p + 1 < st->n_prompt) {
+                st->token = a.prompt[p + 1];
+            } else {
+                if (st->produced < st->max_out) a.tokens[st->produced] = r.i;
+                st->produced += 1;
+                st->token = r.i;
+            }
+            st->pos += 1;
+        }
+    }
+}
+
 template <int G, int R, int EPI>
 struct Tile {
     static constexpr int RPS = 64 / G;                         // rows per wave step
@@ -154,7 +237,13 @@ __global__ __launch_bounds__(kThreads, 8) void q4_gemv_kernel(GemvArgs a, int n_
     // the weights (loads return in issue order); K <= 12288 stays in
     // registers across the weight issue (K <= 4096 with a norm gain)
     constexpr int kXR = XS == cwi::XS_RMSNORM ? 1 : 3;
-    const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
+    const float *xsrc = a.x;
+    if (a.x_tok) {  // the embedding row of the device-resident token
+        uint32_t t = *a.x_tok;
+        t = t < (uint32_t)a.tok_rows ? t : (uint32_t)(a.tok_rows - 1);
+        xsrc = a.x + (size_t)t * K;
+    }
+    const float4 *x4 = reinterpret_cast<const float4 *>(xsrc);
     const float4 *w4 = reinterpret_cast<const float4 *>(a.norm_w);
     float4 xv[kXR], wn[kXR];
 #pragma unroll
@@ -222,6 +311,15 @@ __global__ __launch_bounds__(kThreads, 8) void q4_gemv_kernel(GemvArgs a, int n_
     }
 
     // ---- stream the weights ----
+    const float *rsrc = a.resid;
+    if constexpr (EPI == cwi::EPI_ADD) {
+        if (a.resid_tok) {  // the residual is the embedding row (first layer)
+            uint32_t t = *a.resid_tok;
+            t = t < (uint32_t)a.tok_rows ? t : (uint32_t)(a.tok_rows - 1);
+            rsrc = a.resid + (size_t)t * a.N;
+        }
+    }
+    Best best{kNegInit, 0u};  // EPI_ARGMAX: this lane's best row so far
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
@@ -279,8 +377,11 @@ __global__ __launch_bounds__(kThreads, 8) void q4_gemv_kernel(GemvArgs a, int n_
                             if (row < a.N) {
                                 if constexpr (EPI == cwi::EPI_STORE) {
                                     a.y[row] = acc[rr];
+                                } else if constexpr (EPI == cwi::EPI_ARGMAX) {
+                                    a.y[row] = acc[rr];
+                                    best = better(best, Best{acc[rr], (uint32_t)row});
                                 } else if constexpr (EPI == cwi::EPI_ADD) {
-                                    a.y[row] = a.resid[row] + acc[rr];
+                                    a.y[row] = rsrc[row] + acc[rr];
                                 } else {
                                     const float g = acc[rr], up = acc[rr + T::NR];
                                     const float sg = g / (1.0f + expf(-g));
@@ -299,6 +400,7 @@ __global__ __launch_bounds__(kThreads, 8) void q4_gemv_kernel(GemvArgs a, int n_
             }
         }
     }
+    if constexpr (EPI == cwi::EPI_ARGMAX) argmax_tail(a, best, tid, lane, wave);
 }
 
 typedef void (*gemv_fn)(GemvArgs, int);
@@ -308,6 +410,9 @@ gemv_fn pick_epi(int epi) {
     switch (epi) {
         case cwi::EPI_STORE: return q4_gemv_kernel<G, R, XS, cwi::EPI_STORE, PD>;
         case cwi::EPI_ADD: return q4_gemv_kernel<G, R, XS, cwi::EPI_ADD, PD>;
+        case cwi::EPI_ARGMAX:
+            if constexpr (XS == cwi::XS_RMSNORM) return q4_gemv_kernel<G, R, XS, cwi::EPI_ARGMAX, PD>;
+            return nullptr;
         default:
             if constexpr (R % 2 == 0) return q4_gemv_kernel<G, R, XS, cwi::EPI_SWIGLU, PD>;
             return nullptr;
@@ -377,9 +482,10 @@ int occupancy(gemv_fn fn, int lds, int *blocks) {
 }
 
 const char *label_of(int xs, int epi) {
-    static const char *names[2][3] = {
-        {"q4_gemv", "q4_gemv_add", "q4_gemv_swiglu"},
-        {"q4_gemv_rmsnorm", "q4_gemv_rmsnorm_add", "q4_gemv_rmsnorm_swiglu"}};
+    static const char *names[2][4] = {
+        {"q4_gemv", "q4_gemv_add", "q4_gemv_swiglu", "q4_gemv_argmax"},
+        {"q4_gemv_rmsnorm", "q4_gemv_rmsnorm_add", "q4_gemv_rmsnorm_swiglu",
+         "q4_gemv_rmsnorm_argmax"}};
     return names[xs][epi];
 }
 
@@ -418,6 +524,26 @@ int launch_q4_gemv(cw_ctx *ctx, XSrc xs, Epi epi, const GemvArgs &a) {
     const int cap = (long_stream ? 4 : 2) * ctx->n_cu;
     if (grid > cap) grid = cap;
     return launch(ctx, label_of(xs, epi), fn, dim3(grid), dim3(kThreads), lds, a, n_tiles);
+}
+
+size_t lm_argmax_scratch_bytes(const cw_ctx *ctx) {
+    // bests for up to four workgroups per CU (launch_q4_gemv's largest grid),
+    // then the counter on its own 128-byte line
+    return (size_t)4 * ctx->n_cu * 8 + 256;
+}
+
+int launch_lm_head_argmax(cw_ctx *ctx, GemvArgs g, void *scratch, uint32_t *out_dev,
+                          GenState *state, const uint32_t *prompt_dev, uint32_t *tokens_out_dev) {
+    const size_t cap = (size_t)4 * ctx->n_cu;
+    unsigned char *base = static_cast<unsigned char *>(scratch);
+    g.am_v = reinterpret_cast<float *>(base);
+    g.am_i = reinterpret_cast<uint32_t *>(base + cap * 4);
+    g.am_cnt = reinterpret_cast<unsigned *>(base + ((cap * 8 + 127) & ~(size_t)127));
+    g.am_out = out_dev;
+    g.state = state;
+    g.prompt = prompt_dev;
+    g.tokens = tokens_out_dev;
+    return launch_q4_gemv(ctx, XS_RMSNORM, EPI_ARGMAX, g);
 }
 
 }  // namespace cwi
