@@ -139,9 +139,10 @@ def bench_prefill_8b(ctx, m, cfg, P=512, reps=3):
         "gemm_ms": round(gemm_ms, 3),
         "mfma_util": round(lin / (gemm_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
         "mfma_util_note": "useful linear flops / GEMM kernel time (incl. split-K reduce) / "
-                          "2.5 PFLOP/s dense fp16; each Q4 block issues three f16 MFMAs "
-                          "(x_hi W_hi, x_hi W_lo, x_lo W_hi: exact split operands for "
-                          "f32-level parity), so the matrix pipes run 3x the useful flops",
+                          "2.5 PFLOP/s dense fp16; each 16-wide k slice issues two f16 "
+                          "MFMAs (x_hi and x_lo against the exact q - 8, for f32-level "
+                          "parity; the block scale goes on each block's f32 sum), so the "
+                          "matrix pipes run 2x the useful flops",
         "kernel_ms": {k: round(v, 3) for k, v in prof.items()},
     }
 

@@ -16,9 +16,6 @@ maps it to ids and back, and decides when to stop.
 """
 from tokenizers import Tokenizer
 
-# cw.STEP_GRAPH: a decode step replayed from its captured HIP graph
-STEP_GRAPH = 1
-
 # end-of-turn markers looked up in the tokenizer's vocabulary (wasm.rs:48-51)
 EOS_TOKENS = ("<|im_end|>", "<|endoftext|>")
 
@@ -96,8 +93,8 @@ class LocalChat:
                 nxt = self.model.step(t, pos)
         # after the batched prompt phase the decode state lives on the device:
         # each further token is one replay of the captured step (the
-        # benchmarked path), read back as the device loop's newest id
-        graph = batched_prefill and hasattr(self.model, "decode_async")
+        # benchmarked path), whose argmax comes back as one 4-byte read
+        graph = batched_prefill and hasattr(self.model, "decode_next")
         pos = len(ids)
         produced, shown = [], ""
         for i in range(max_tokens):
@@ -112,8 +109,7 @@ class LocalChat:
                 shown = full
             if i + 1 < max_tokens:  # the step after the last token would be unused
                 if graph:
-                    self.model.decode_async(1, mode=STEP_GRAPH)
-                    nxt = int(self.model.tokens(i + 1)[-1])
+                    nxt = self.model.decode_next()
                 else:
                     nxt = self.model.step(nxt, pos)
                 pos += 1

@@ -276,6 +276,7 @@ int launch_argmax(cw_ctx *ctx, const float *logits, int n, uint32_t *out_dev, vo
 // GGUF Q4_0; EPI_SWIGLU reads a second matrix (B) and stores silu(A x) * (B x).
 struct GemmArgs {
     const uint16_t *xhi, *xlo;  // [M][K] f16 bits, row m scaled by 1 / rowscale[m]
+                                // (allocated for gemm_x_elems(M, K))
     const float *rowscale;      // [M] powers of two
     const uint16_t *sA;
     const uint8_t *qA;
@@ -290,6 +291,10 @@ struct GemmArgs {
 // K splits the GEMM uses for this shape (the partial workspace holds
 // splits * M * N floats)
 int gemm_splits(const cw_ctx *ctx, Epi epi, int M, int N, int K);
+// Elements each of GemmArgs::xhi / xlo must hold for M rows of K: whole
+// 128-row tiles plus one block (the GEMM's DMA reads them; rows past M are
+// never stored to y, so they need no values)
+size_t gemm_x_elems(int M, int K);
 // token ids on the device (validated < vocab by the caller)
 int launch_embed_rows(cw_ctx *ctx, const float *table, int dim, const uint32_t *tok_dev, int n,
                       float *out);

@@ -368,7 +368,13 @@ int tensor_bytes(const cw_gguf *g, const char *name, const TensorRec **out, cons
                   (unsigned long long)t->n_elems, lay->qk);
         return CW_ERR_FORMAT;
     }
-    const uint64_t nbytes = t->n_elems / lay->qk * lay->bytes;
+    const uint64_t n_blocks = t->n_elems / lay->qk;
+    if (n_blocks > UINT64_MAX / lay->bytes) {
+        set_error("tensor %s: %llu elements overflow its byte count", name,
+                  (unsigned long long)t->n_elems);
+        return CW_ERR_FORMAT;
+    }
+    const uint64_t nbytes = n_blocks * lay->bytes;
     const uint64_t avail = g->size - g->data_start;
     if (t->offset > avail || nbytes > avail - t->offset) {
         set_error("tensor %s: bytes [%llu, +%llu) run past the data section (%llu bytes)", name,

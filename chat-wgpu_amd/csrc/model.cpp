@@ -70,6 +70,7 @@ struct cw_model {
     float *part = nullptr;
     void *argmax_scratch = nullptr;
     void *lm_scratch = nullptr;  // the LM head's fused argmax (counter zero between launches)
+    int host_pos = 0;            // the device state's pos, mirrored (every step advances it by 1)
     GenState *state = nullptr;
     uint32_t *prompt_dev = nullptr, *tokens_dev = nullptr, *argmax_out = nullptr;
     bool finalized = false;
@@ -362,6 +363,7 @@ int run_steps(cw_model *m, int n, int mode) {
         set_error("unknown step mode %d", mode);
         return CW_ERR_ARG;
     }
+    m->host_pos += n;
     return CW_OK;
 }
 
@@ -490,8 +492,8 @@ int ensure_prefill(cw_model *m, int n) {
     CW_TRY(al((size_t)n * m->q_dim * 4, (void **)&m->pf_q));
     CW_TRY(al((size_t)n * m->q_dim * 4, (void **)&m->pf_attn));
     CW_TRY(al((size_t)n * c.hidden * 4, (void **)&m->pf_act));
-    CW_TRY(al((size_t)n * wide * 2, (void **)&m->pf_hi));
-    CW_TRY(al((size_t)n * wide * 2, (void **)&m->pf_lo));
+    CW_TRY(al(gemm_x_elems(n, (int)wide) * 2, (void **)&m->pf_hi));
+    CW_TRY(al(gemm_x_elems(n, (int)wide) * 2, (void **)&m->pf_lo));
     CW_TRY(al((size_t)n * 4, (void **)&m->pf_rowscale));
     // split-K workspace: the largest splits x M x N of the unfused GEMMs
     size_t part = 0;
@@ -576,6 +578,7 @@ int enqueue_prefill(cw_model *m, int n, int start) {
 int set_state(cw_model *m, const GenState &s) {
     CW_HIP(hipMemcpyAsync(m->state, &s, sizeof s, hipMemcpyHostToDevice, m->ctx->stream));
     CW_HIP(hipStreamSynchronize(m->ctx->stream));
+    m->host_pos = s.pos;
     return CW_OK;
 }
 
@@ -957,6 +960,7 @@ int cw_model_step(cw_model *m, uint32_t token, int pos, uint32_t *argmax_out) {
     GenState s{pos, token, pos, 0, 0, 0};
     CW_TRY(set_state(m, s));
     CW_TRY(enqueue_step(m));
+    m->host_pos = pos + 1;
     CW_TRY(launch_rmsnorm(m->ctx, last_hidden(m), m->final_norm, 1, m->cfg.dim, m->cfg.eps,
                           m->hidden_out));
     uint32_t r = 0;
@@ -1120,13 +1124,25 @@ int cw_model_decode_async(cw_model *m, int n_steps, int mode) {
     CW_CHECK_ARG(m != nullptr && n_steps >= 0, "cw_model_decode_async: bad argument");
     CW_TRY(refuse_recording(m, "cw_model_decode_async"));
     CW_TRY(require_final(m, "cw_model_decode_async"));
-    GenState s{};
-    CW_HIP(hipMemcpyAsync(&s, m->state, sizeof s, hipMemcpyDeviceToHost, m->ctx->stream));
-    CW_HIP(hipStreamSynchronize(m->ctx->stream));
-    CW_CHECK_ARG(s.pos + n_steps <= m->cfg.max_seq,
-                 "cw_model_decode_async: %d steps from pos %d exceed max_seq %d", n_steps, s.pos,
-                 m->cfg.max_seq);
+    CW_CHECK_ARG(m->host_pos + n_steps <= m->cfg.max_seq,
+                 "cw_model_decode_async: %d steps from pos %d exceed max_seq %d", n_steps,
+                 m->host_pos, m->cfg.max_seq);
     return run_steps(m, n_steps, mode);
+}
+
+int cw_model_decode_next(cw_model *m, uint32_t *next_out) {
+    CW_CHECK_ARG(m && next_out, "cw_model_decode_next: null argument");
+    CW_TRY(refuse_recording(m, "cw_model_decode_next"));
+    CW_TRY(require_final(m, "cw_model_decode_next"));
+    CW_CHECK_ARG(m->host_pos < m->cfg.max_seq, "cw_model_decode_next: pos %d at max_seq %d",
+                 m->host_pos, m->cfg.max_seq);
+    CW_TRY(run_steps(m, 1, CW_STEP_GRAPH));
+    // the step's LM head leaves its argmax here: one 4-byte read per token
+    uint32_t r = 0;
+    CW_HIP(hipMemcpyAsync(&r, m->argmax_out, 4, hipMemcpyDeviceToHost, m->ctx->stream));
+    CW_HIP(hipStreamSynchronize(m->ctx->stream));
+    *next_out = r;
+    return CW_OK;
 }
 
 int cw_model_profile_step(cw_model *m, int64_t *ticks, int max_n, int *n_out, double *tick_hz) {

@@ -8,16 +8,17 @@
 //
 // Precision.  The GEMM and attention must match the f32 per-token path, so no
 // operand is rounded below what the reference computes with:
-//  * GEMM: every Q4_0 weight (q - 8) d enters the f16 MFMAs exactly, as two
-//    f16 parts; each f32 activation row is split into f16 hi + lo (22
-//    significant bits) after an exact power-of-two row scaling (details at
-//    the kernel).  The MFMAs accumulate in f32.
+//  * GEMM: every Q4_0 quant (q - 8) enters the f16 MFMAs exactly and the
+//    block scale multiplies each block's f32 sum; each f32 activation row is
+//    split into f16 hi + lo (22 significant bits) after an exact power-of-two
+//    row scaling (details at the kernel).  The MFMAs accumulate in f32.
 //  * Attention: K and V are f16 in the cache and enter f16 MFMAs exactly; q
 //    and the softmax weights p are split into f16 hi + lo the same way.
 //
-// MFMA v_mfma_f32_16x16x32_f16: lane l holds A[l % 16][8 (l / 16) + j]
-// and B[8 (l / 16) + j][l % 16] (j = 0..7) and receives D[4 (l / 16) + r][l % 16]
-// (r = 0..3); any k order shared by A and B is valid.
+// MFMA v_mfma_f32_16x16x32_f16 (attention): lane l holds A[l % 16][8 (l / 16)
+// + j] and B[8 (l / 16) + j][l % 16] (j = 0..7) and receives
+// D[4 (l / 16) + r][l % 16] (r = 0..3); any k order shared by A and B is
+// valid.
 
 #include <cmath>
 
@@ -29,6 +30,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kT = 256;  // threads per workgroup (4 waves)
 
@@ -132,23 +134,36 @@ __global__ __launch_bounds__(kT) void split_rows_kernel(const float *__restrict_
 //  * x: per row m a power of two 2^e_m brings max|x| into [2^8, 2^9) (the
 //    split kernel), then x 2^-e_m = x_hi + x_lo with x_hi = f16(.) and x_lo
 //    = f16(remainder): 22 significant bits, no overflow;
-//  * W: the block scale d (f16, 11 bits) = d_hi + d_lo with d_hi rounded to
-//    8 bits and d_lo the 3-bit remainder, and each weight (q - 8) d =
-//    (q - 8) d_hi + (q - 8) d_lo, both parts exact in f16 (at most 11 and 6
-//    significant bits) for |d| < 8192.
-// y = 2^e_m (x_hi W_hi + x_hi W_lo + x_lo W_hi): three f16 MFMAs per
-// 32-wide block accumulate straight into the f32 accumulators, so there is
-// no per-block scaling on the vector ALUs; the dropped x_lo W_lo term is
-// below 2^-19 of each product.
+//  * W: the quants as q - 8 (small integers, exact in f16); the block scale
+//    d is applied to the block's f32 sum, not to the operand.
+// Per block b: t = sum over its 32 k of (x_hi + x_lo) (q - 8), two f16 MFMAs
+// per 16-wide k slice (every product exact, the sum in f32); then
+// acc += d_b t, one f32 FMA per output element and block.  y = 2^e_m acc.
+// This is the reference's sum of d (q - 8) x over the blocks with the
+// rounding of an f32 computation (q4.wgsl:25-82 forms d (q - 8) per weight;
+// here d multiplies each block's partial sum).
+//
+// Matrix cores: v_mfma_f32_32x32x16_f16 (lane l holds A[l % 32][8 (l / 32)
+// + j] and B[8 (l / 32) + j][l % 32], j = 0..7, and receives
+// D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32], r = 0..15).  A Q4 block is two
+// k slices: the low nibbles of its bytes 0..15 (elements 0..15) and the high
+// nibbles (elements 16..31); the lanes of half g of the wave take bytes
+// 8g..8g+7, i.e. elements 8g + j of the low slice and 16 + 8g + j of the
+// high one, so one 8-byte read gives a lane both slices of B.
 //
 // Tiling: workgroup tile 128 (rows of x) x 128 (rows of W), four waves in
-// 2 x 2 of 64 x 64 (4 x 4 MFMA tiles of 16 x 16).  K runs one Q4 block per
-// stage, double-buffered in LDS (the x tile hi/lo and the W tile hi/lo, 64 B
-// rows with XOR-swizzled 16-byte chunks against bank conflicts); the global
-// loads run two stages ahead in registers while the waves run 48 MFMAs per
-// stage from LDS.  64 KB of LDS and at most 256 registers per lane let two
-// workgroups share a CU, so one workgroup's barrier and load waits overlap
-// the other's MFMAs.
+// 2 x 2 of 64 x 64 (2 x 2 MFMA tiles of 32 x 32).  A K stage is two Q4
+// blocks.  Its x tile (hi and lo, 128 rows x 64 k) and the raw quants of its
+// W tile go from global memory straight into LDS (global_load_lds, 16 bytes
+// per lane, no registers), double-buffered: stage s + 1 is in flight while
+// the waves compute stage s, with one barrier per stage.  The DMA writes LDS
+// in lane order, so the x rows' XOR swizzle (16-byte chunk c of row r at
+// slot c ^ ((r / 2) % 8): conflict-free fragment reads) is made by choosing
+// which global chunk each lane loads.  The block scales come through
+// registers and are stored as f32.  Each wave dequantizes its own B
+// fragments from the nibbles (perm into the f16 1024 + q, minus 1032: exact).
+// 74 KB of LDS (two stage buffers) and at most 256 registers per lane let
+// two workgroups share a CU.
 //
 // SwiGLU: the W tile is 64 gate rows + the same 64 up rows; each wave holds
 // 32 gate and the matching 32 up columns, so silu(g) * u is formed in
@@ -160,119 +175,141 @@ __global__ __launch_bounds__(kT) void split_rows_kernel(const float *__restrict_
 // tiles to fill every CU twice, K is split over S workgroups that write f32
 // partials; a second kernel adds them in a fixed order (deterministic) with
 // the epilogue.
-constexpr int kGM = 128, kGN = 128;           // workgroup tile
-constexpr int kGRow = 64;                     // LDS row bytes: 32 f16
-constexpr int kPre = 2;                       // stages of global loads in flight
-
-// Byte offset of 16-byte chunk c (0..3) in LDS row `row`: the chunk index is
-// XOR-swizzled by (row / 2) % 4, so the 4 lanes per row of a staging store
-// and the 16 rows of a fragment read both spread over distinct bank groups.
-__device__ __forceinline__ int swz(int row, int c) { return (c ^ ((row >> 1) & 3)) << 4; }
-constexpr int kGA = kGM * kGRow;              // one of x hi / x lo
-constexpr int kGB = kGN * kGRow;              // one of W hi / W lo
-constexpr int kGBuf = 2 * kGA + 2 * kGB;      // 40 KB per stage
+constexpr int kGM = 128;               // workgroup tile rows (of x)
+constexpr int kSB = 2;                 // Q4 blocks per K stage
+constexpr int kXRow = kSB * 32 * 2;    // LDS bytes of one x row (one half) per stage
+constexpr int kXHalf = kGM * kXRow;    // x hi (then x lo): 16 KB
 constexpr int kMaxSplit = 8;
+static_assert(kXRow == 128, "the x swizzle assumes 8 chunks of 16 bytes per row");
+
+// Tile geometry for WN waves along N (2 x WN waves): BN rows of W (LDS
+// columns) per tile, one W unit (column, block) per thread per stage.
+template <int WN>
+struct GT {
+    static constexpr int WAVES = 2 * WN, THREADS = 64 * WAVES;
+    static constexpr int BN = 64 * WN;
+    static constexpr int WQ = 2 * kXHalf;          // quants [block][col] x 16 B
+    static constexpr int WD = WQ + kSB * BN * 16;  // d as f32 [block][col]
+    static constexpr int BUF = WD + kSB * BN * 4;  // one stage: 37 KB (WN 2), 39.5 KB (WN 3)
+    static_assert(kSB * BN == THREADS, "one W unit per thread per stage");
+    static_assert(2 * BUF * 2 <= 160 * 1024, "two workgroups per CU");
+};
+
+typedef __attribute__((address_space(3))) unsigned char lds_u8;
+
+// One 16-byte-per-lane global -> LDS DMA: lane i's 16 bytes land at LDS byte
+// lds_off + 16 i (lds_off wave-uniform, in M0).  Written as asm so the
+// compiler's wait-count pass does not track it: its own waits (for register
+// loads) stay correct, being only stricter with loads it does not count, and
+// it adds none before LDS reads; the kernel orders the DMA itself with
+// counted vmcnt waits and a barrier.  M0 is written only here (the kernel has
+// no other M0 user).
+__device__ __forceinline__ void dma16(const void *src, unsigned char *lds_dst) {
+    const uint32_t off =
+        __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_u8 *)lds_dst);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(src), "s"(off)
+                 : "memory", "m0");
+}
 
 __device__ __forceinline__ float f16_bits_val(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
-// Nibbles of a quant dword w at bits 4h + {0, 8, 16, 24} (h = 0: the low
-// nibbles, elements 4i..4i+3 of the dword's bytes; h = 1: the high ones)
-// -> the f16 pairs (q - 8) of elements (0, 1) and (2, 3), exactly: 0x6400 | q
-// is the f16 1024 + q.
-__device__ __forceinline__ void nib_pairs(uint32_t w, int h, f16x2 &p01, f16x2 &p23) {
-    const uint32_t s = w >> (4 * h);
-    const uint32_t a = (s & 0x000F000Fu) | 0x64006400u;         // bytes 0, 2
-    const uint32_t b = ((s >> 8) & 0x000F000Fu) | 0x64006400u;  // bytes 1, 3
-    const f16x2 off = {(_Float16)1032.0f, (_Float16)1032.0f};
-    p01 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(b, a, 0x05040100u)) - off;
-    p23 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(b, a, 0x07060302u)) - off;
+// LDS byte offset of 16-byte chunk c (0..7) of x row `row` within one half
+__device__ __forceinline__ int xoff(int row, int c) {
+    return row * kXRow + ((c ^ ((row >> 1) & 7)) << 4);
 }
 
-// One stage in registers: 4 x 16 B of x per thread (128 rows x 64 B, hi
-// then lo) and the 16 quant bytes and the f16 scale of one W row's block
-// (thread pairs share a row: the even thread dequantizes its low nibbles,
-// the odd one its high nibbles).  Native vector registers: an array of
-// HIP's uint4 class is copied with memcpy and stays in scratch memory.
-template <bool SWI>
-__device__ __forceinline__ void w_row(const cwi::GemmArgs &a, int n0, int vc, int *n,
+// W tile column -> weight row and its matrix (SwiGLU: BN / 2 gate rows, then
+// the same up rows)
+template <bool SWI, int BN>
+__device__ __forceinline__ void w_col(const cwi::GemmArgs &a, int n0, int col, int *n,
                                       const uint8_t **q, const uint16_t **s) {
     if constexpr (SWI) {
-        const bool up = vc >= kGN / 2;
-        *n = n0 + (vc & (kGN / 2 - 1));
+        const bool up = col >= BN / 2;
+        *n = n0 + (up ? col - BN / 2 : col);
         *q = up ? a.qB : a.qA;
         *s = up ? a.sB : a.sA;
     } else {
-        *n = n0 + vc;
+        *n = n0 + col;
         *q = a.qA;
         *s = a.sA;
     }
 }
 
-// Block kb of the tile; at or past kb_end the scale is 0 (loads clamped in
-// range, so every operand stays finite and the block adds exact zeros).
-template <bool SWI>
-__device__ __forceinline__ void gstage_load(const cwi::GemmArgs &a, int nb, int kb, int kb_end,
-                                            int m0, int n0, int tid, u32x4 (&sx)[4], u32x4 &sq,
-                                            uint32_t &sd) {
-    const int blk = min(kb, nb - 1);
+// The x DMAs of one workgroup stage: 2 halves x 16 groups of 8 rows, one
+// 1 KB DMA each, wave w taking groups t = w, w + WAVES, ...  Lane i of a
+// group fills slot i % 8 of row 8 grp + i / 8 with the chunk the swizzle puts
+// there: chunk c = (i % 8) ^ ((row / 2) % 8), which for a given lane only
+// depends on the parity of grp.  xl[p] is the lane's element offset for
+// parity p (row and chunk within the stage); the stage adds 32 kbs.
+template <int WN>
+__device__ __forceinline__ void stage_x(const cwi::GemmArgs &a, const size_t (&xl)[2], int kbs,
+                                        int wave, unsigned char *buf) {
+    constexpr int WAVES = GT<WN>::WAVES;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int f = tid + u * kT;              // 0..1023
-        const int half = f >> 9;                 // 0: hi, 1: lo
-        const int row = (f >> 2) & (kGM - 1), c = f & 3;
-        const int m = min(m0 + row, a.M - 1);
-        const uint16_t *src = half ? a.xlo : a.xhi;
-        sx[u] = *reinterpret_cast<const u32x4 *>(src + (size_t)m * a.K + (size_t)blk * 32 + c * 8);
+    for (int u = 0; u < (32 + WAVES - 1) / WAVES; ++u) {
+        const int t = wave + u * WAVES;  // wave-uniform
+        if (u < 32 / WAVES || t < 32) {  // (only the last round can fall short)
+            const int half = t >> 4, grp = t & 15;
+            const uint16_t *base = half ? a.xlo : a.xhi;
+            dma16(base + xl[grp & 1] + ((size_t)grp * 8 * a.K + (size_t)kbs * 32),
+                  buf + half * kXHalf + grp * 1024);
+        }
     }
+}
+
+// W of one stage, unit t = block * BN + column: its 16 quant bytes and its
+// scale, as loaded (two loads; past kb_end the last block's, never used:
+// that block's MFMAs are skipped)
+struct WUnit {
+    uint4 q;
+    uint32_t d;
+};
+template <bool SWI, int BN>
+__device__ __forceinline__ WUnit stage_w(const cwi::GemmArgs &a, int nb, int kb, int kb_end,
+                                         int n0, int tid) {
     int n;
     const uint8_t *q;
     const uint16_t *s;
-    w_row<SWI>(a, n0, tid >> 1, &n, &q, &s);
-    const size_t o = (size_t)min(n, a.N - 1) * nb + blk;
-    sq = *reinterpret_cast<const u32x4 *>(q + o * 16);
-    const uint32_t dd = s[o];  // loaded unconditionally, then selected
-    sd = kb < kb_end ? dd : 0u;
+    w_col<SWI, BN>(a, n0, tid % BN, &n, &q, &s);
+    const size_t o = (size_t)min(n, a.N - 1) * nb + min(kb + tid / BN, kb_end - 1);
+    return WUnit{*reinterpret_cast<const uint4 *>(q + o * 16), s[o]};
 }
 
-__device__ __forceinline__ void gstage_store(const u32x4 (&sx)[4], u32x4 sq, uint32_t sd,
-                                             unsigned char *buf, int tid) {
+// Workgroup barrier on LDS data only: __syncthreads would also wait for
+// every global load in flight (the W loads two stages ahead)
+__device__ __forceinline__ void lds_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Nibbles (4 bits at byte offsets 0..3 of t) -> f16 pairs (q - 8) of bytes
+// (0, 1) and (2, 3): 0x64 over a nibble is the f16 1024 + q
+__device__ __forceinline__ void nib4(uint32_t t, f16x2 &p01, f16x2 &p23) {
+    const f16x2 off = {(_Float16)1032.0f, (_Float16)1032.0f};
+    p01 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, t, 0x04010400u)) - off;
+    p23 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, t, 0x04030402u)) - off;
+}
+
+// 8 quant bytes (w0, w1) -> B fragments (q - 8, exact in f16) of the low
+// slice (ks 0) and the high slice (ks 1)
+__device__ __forceinline__ void dequant8(uint32_t w0, uint32_t w1, f16x8 (&bq)[2]) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int f = tid + u * kT;
-        const int half = f >> 9;
-        const int row = (f >> 2) & (kGM - 1), c = f & 3;
-        *reinterpret_cast<u32x4 *>(buf + half * kGA + row * kGRow + swz(row, c)) = sx[u];
+    for (int ks = 0; ks < 2; ++ks) {
+        const uint32_t t0 = (w0 >> (4 * ks)) & 0x0F0F0F0Fu, t1 = (w1 >> (4 * ks)) & 0x0F0F0F0Fu;
+        f16x2 p[4];
+        nib4(t0, p[0], p[1]);
+        nib4(t1, p[2], p[3]);
+        bq[ks] = __builtin_bit_cast(f16x8, (u32x4){__builtin_bit_cast(uint32_t, p[0]),
+                                                   __builtin_bit_cast(uint32_t, p[1]),
+                                                   __builtin_bit_cast(uint32_t, p[2]),
+                                                   __builtin_bit_cast(uint32_t, p[3])});
     }
-    // d = d_hi + d_lo: d_hi the f32 d rounded to 8 significant bits
-    const float d = f16_bits_val(sd);
-    uint32_t u = __builtin_bit_cast(uint32_t, d);
-    u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
-    const float dh = __builtin_bit_cast(float, u);
-    const _Float16 h16 = (_Float16)dh, l16 = (_Float16)(d - dh);  // both exact
-    const f16x2 dh2 = {h16, h16}, dl2 = {l16, l16};
-    // elements 16 h .. 16 h + 15 of the block: nibble half h of bytes 0..15
-    const int vc = tid >> 1, h = tid & 1;
-    u32x4 ph[2], pl[2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        f16x2 p01, p23;
-        nib_pairs(sq[i], h, p01, p23);
-        const int k = 4 * i;  // elements k..k+3 of this half
-        const f16x2 h01 = p01 * dh2, h23 = p23 * dh2, l01 = p01 * dl2, l23 = p23 * dl2;
-        ph[k >> 3][(k & 7) >> 1] = __builtin_bit_cast(uint32_t, h01);
-        ph[k >> 3][((k & 7) >> 1) + 1] = __builtin_bit_cast(uint32_t, h23);
-        pl[k >> 3][(k & 7) >> 1] = __builtin_bit_cast(uint32_t, l01);
-        pl[k >> 3][((k & 7) >> 1) + 1] = __builtin_bit_cast(uint32_t, l23);
-    }
-    unsigned char *wh = buf + 2 * kGA + vc * kGRow;
-    unsigned char *wl = wh + kGB;
-    const int o0 = swz(vc, 2 * h), o1 = swz(vc, 2 * h + 1);
-    *reinterpret_cast<u32x4 *>(wh + o0) = ph[0];
-    *reinterpret_cast<u32x4 *>(wh + o1) = ph[1];
-    *reinterpret_cast<u32x4 *>(wl + o0) = pl[0];
-    *reinterpret_cast<u32x4 *>(wl + o1) = pl[1];
 }
 
 // Tile t of MT x NT x S -> (m tile, n tile, split), XCD-grouped when the
@@ -287,102 +324,158 @@ __device__ __forceinline__ void tile_of(int w, int total, int NT, int MT, int *m
     *sp = r / MT;
 }
 
-// OUT: 0 = the epilogue EPI into y, 1 = f32 partial of split sp into part
-template <int EPI, int OUT>
-__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(2, 2))) void q4_gemm_kernel(
-    cwi::GemmArgs a, int MT, int NT, int S) {
+// OUT: 0 = the epilogue EPI into y, 1 = f32 partial of split sp into part.
+// x hi / lo hold ceil(M / 128) * 128 rows plus 32 elements (the DMA reads
+// whole row tiles and, for an odd final block, one block past the split).
+template <int EPI, int OUT, int WN>
+__global__ __launch_bounds__(GT<WN>::THREADS) __attribute__((amdgpu_waves_per_eu(WN, WN)))
+void q4_gemm_kernel(cwi::GemmArgs a, int MT, int NT, int S) {
     constexpr bool SWI = EPI == cwi::EPI_SWIGLU;
-    extern __shared__ __attribute__((aligned(16))) unsigned char glds[];
+    using G = GT<WN>;
+    constexpr int BN = G::BN;
+    // the two stage buffers are separate LDS objects, and the stage loop
+    // below is unrolled by two so each access names one of them
+    __shared__ __attribute__((aligned(16))) unsigned char lds_a[G::BUF];
+    __shared__ __attribute__((aligned(16))) unsigned char lds_b[G::BUF];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int li = lane & 15, lg = lane >> 4;
+    const int li = lane & 31, lg = lane >> 5;
     int mt, nt, sp;
     tile_of(blockIdx.x, MT * NT * S, NT, MT, &mt, &nt, &sp);
-    const int m0 = mt * kGM, n0 = nt * (SWI ? kGN / 2 : kGN);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = mt * kGM, n0 = nt * (SWI ? BN / 2 : BN);
+    const int wm = wave / WN, wn = wave % WN;
     const int nb = a.K >> 5;
-    // this split's blocks [kb0, kb1), one per stage
-    const int per = (nb + S - 1) / S;
-    const int kb0 = sp * per, kb1 = min(nb, kb0 + per);
-    const int n_st = kb1 - kb0;
+    // this split's blocks [kb0, kb1), two per stage
+    const int per = (((nb + S - 1) / S) + kSB - 1) / kSB * kSB;
+    const int kb0 = min(nb, sp * per), kb1 = min(nb, kb0 + per);
+    const int n_st = (kb1 - kb0 + kSB - 1) / kSB;
 
-    // column tile j of this wave -> virtual column (LDS W row) of its lane
-    int vcol[4];
+    // LDS column of this lane in column tile j
+    int col[2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-        vcol[j] = SWI ? (j < 2 ? wn * 32 + j * 16 : kGN / 2 + wn * 32 + (j - 2) * 16) + li
-                      : wn * 64 + j * 16 + li;
-
-    f32x4 acc[4][4];
+    for (int j = 0; j < 2; ++j)
+        col[j] = (SWI ? j * (BN / 2) + wn * 32 : wn * 64 + j * 32) + li;
+    // this lane's x DMA element offsets (row and chunk) for even / odd groups
+    size_t xl[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    // a ring of kPre register stages: the loads of stage s + 1 + kPre go out
-    // right after stage s + 1 is written to LDS, kPre stages ahead of use;
-    // every load is unconditional (past the end a stage re-loads the last
-    // block, unused), which keeps the registers out of scratch and the loads
-    // where they are issued
-    u32x4 sx[kPre][4], sq[kPre];
-    uint32_t sd[kPre];
-    if (n_st > 0) {
-        gstage_load<SWI>(a, nb, kb0, kb1, m0, n0, tid, sx[0], sq[0], sd[0]);
-        gstage_store(sx[0], sq[0], sd[0], glds, tid);
+    for (int p = 0; p < 2; ++p) {
+        const int row = p * 8 + (lane >> 3);
+        const int c = (lane & 7) ^ ((row >> 1) & 7);
+        xl[p] = (size_t)(m0 + (lane >> 3)) * a.K + (c >> 2) * 32 + (c & 3) * 8;
     }
+
+    f32x16 acc[2][2];
 #pragma unroll
-    for (int u = 0; u < kPre; ++u)
-        gstage_load<SWI>(a, nb, kb0 + min(1 + u, max(n_st - 1, 0)), kb1, m0, n0, tid, sx[u], sq[u],
-                         sd[u]);
-    __syncthreads();
-    for (int s0 = 0; s0 < n_st; s0 += kPre) {
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int u = 0; u < kPre; ++u) {
-            const int s = s0 + u;
-            if (s < n_st) {
-                const unsigned char *cur = glds + (s & 1) * kGBuf;
-                f16x8 A[4][2], B[4][2];
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int row = wm * 64 + 16 * i + li;
-                    A[i][0] = *reinterpret_cast<const f16x8 *>(cur + row * kGRow + swz(row, lg));
-                    A[i][1] = *reinterpret_cast<const f16x8 *>(cur + kGA + row * kGRow + swz(row, lg));
-                }
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // Pipeline: the x tile of stage st + 1 (L2-resident) is one stage ahead
+    // by DMA; W (streamed from HBM) two stages ahead in a register ring
+    // w[2], stored to LDS one stage ahead.  Loads complete in issue order,
+    // and every stage issues its x DMAs, then its two W loads, so "all but
+    // the last two loads done" means the x tile has landed.  Every stage
+    // issues the same loads (past the split's end they re-read its last
+    // block, in range and unused) and the stage count is padded to even, so
+    // the loop is straight-line code whose wait counts are exact.
+    if (n_st > 0) {
+        WUnit w[2];
+        auto store_w = [&](unsigned char *buf, const WUnit &u) {
+            *reinterpret_cast<uint4 *>(buf + G::WQ + tid * 16) = u.q;
+            *reinterpret_cast<float *>(buf + G::WD + tid * 4) = f16_bits_val(u.d);
+        };
+        // the loads in flight at the loop head come in the loop's own order:
+        // W of stage 1, x of stage 0, W of stage 2
+        w[0] = stage_w<SWI, BN>(a, nb, kb0, kb1, n0, tid);
+        w[1] = stage_w<SWI, BN>(a, nb, kb0 + kSB, kb1, n0, tid);
+        __builtin_amdgcn_sched_barrier(0);
+        stage_x<WN>(a, xl, kb0, wave, lds_a);
+        __builtin_amdgcn_sched_barrier(0);
+        store_w(lds_a, w[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        w[0] = stage_w<SWI, BN>(a, nb, kb0 + 2 * kSB, kb1, n0, tid);
+        // stage st from cur while stage st + 1 goes into nxt; wn holds W of
+        // stage st + 1 and is reloaded with stage st + 3
+        auto step = [&](unsigned char *cur, unsigned char *nxt, WUnit &wnx, int st) {
+            const int kb = kb0 + st * kSB;
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(0x0F72);  // vmcnt(2): x of st landed, W of st + 2 may fly
+            __builtin_amdgcn_sched_barrier(0);
+            lds_barrier();  // stage st published; stage st - 1 retired from nxt
+            store_w(nxt, wnx);
+            stage_x<WN>(a, xl, min(kb + kSB, kb1 - 1), wave, nxt);
+            __builtin_amdgcn_sched_barrier(0);
+            wnx = stage_w<SWI, BN>(a, nb, kb + 3 * kSB, kb1, n0, tid);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int o = vcol[j] * kGRow + swz(vcol[j], lg);
-                    B[j][0] = *reinterpret_cast<const f16x8 *>(cur + 2 * kGA + o);
-                    B[j][1] = *reinterpret_cast<const f16x8 *>(cur + 2 * kGA + kGB + o);
-                }
+            for (int bi = 0; bi < kSB; ++bi) {
+                if (kb + bi < kb1) {  // wave-uniform
+                    f16x8 bq[2][2];
+                    float d[2];
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i][0], B[j][0], acc[i][j], 0, 0, 0);
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i][0], B[j][1], acc[i][j], 0, 0, 0);
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i][1], B[j][0], acc[i][j], 0, 0, 0);
+                    for (int j = 0; j < 2; ++j) {
+                        const uint2 q = *reinterpret_cast<const uint2 *>(
+                            cur + G::WQ + (bi * BN + col[j]) * 16 + 8 * lg);
+                        d[j] = *reinterpret_cast<const float *>(cur + G::WD + (bi * BN + col[j]) * 4);
+                        dequant8(q.x, q.y, bq[j]);
                     }
-                // (after the last stage this fills the idle buffer, not read)
-                gstage_store(sx[u], sq[u], sd[u], glds + ((s + 1) & 1) * kGBuf, tid);
-                gstage_load<SWI>(a, nb, kb0 + min(s + 1 + kPre, n_st - 1), kb1, m0, n0, tid, sx[u],
-                                 sq[u], sd[u]);
-                __builtin_amdgcn_sched_barrier(0);
-                __syncthreads();
+                    // t = x . (q - 8) over the block (x_hi and x_lo, both k
+                    // slices), then acc += d t: the block scale on the f32 sum
+                    f32x16 t[2][2];
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) {
+                        f16x8 ah[2], al[2];
+#pragma unroll
+                        for (int i = 0; i < 2; ++i) {
+                            const int o = xoff(wm * 64 + i * 32 + li, bi * 4 + 2 * ks + lg);
+                            ah[i] = *reinterpret_cast<const f16x8 *>(cur + o);
+                            al[i] = *reinterpret_cast<const f16x8 *>(cur + kXHalf + o);
+                        }
+#pragma unroll
+                        for (int i = 0; i < 2; ++i)
+#pragma unroll
+                            for (int j = 0; j < 2; ++j)
+                                t[i][j] = ks == 0 ? __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                                                        ah[i], bq[j][0], (f32x16){}, 0, 0, 0)
+                                                  : __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                                                        ah[i], bq[j][ks], t[i][j], 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 2; ++i)
+#pragma unroll
+                            for (int j = 0; j < 2; ++j)
+                                t[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                                    al[i], bq[j][ks], t[i][j], 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r)
+                                acc[i][j][r] = __builtin_fmaf(d[j], t[i][j][r], acc[i][j][r]);
+                }
             }
+        };
+        for (int st = 0; st < n_st; st += 2) {
+            step(lds_a, lds_b, w[1], st);
+            step(lds_b, lds_a, w[0], st + 1);
         }
     }
 
-    // lane holds rows 4 lg + r of each row tile, column li of each column tile
-    constexpr int JN = SWI ? 2 : 4;
+    // lane holds rows 8 (r / 4) + 4 lg + r % 4 of each row tile, column li
+    // of each column tile
+    constexpr int JN = SWI ? 1 : 2;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = m0 + wm * 64 + i * 16 + 4 * lg + r;
+        for (int r = 0; r < 16; ++r) {
+            const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
             const float rs = a.rowscale[min(m, a.M - 1)];
 #pragma unroll
             for (int j = 0; j < JN; ++j) {
-                const int n = n0 + (SWI ? wn * 32 + j * 16 : wn * 64 + j * 16) + li;
+                const int n = n0 + (SWI ? wn * 32 : wn * 64 + j * 32) + li;
                 if (m < a.M && n < a.N) {
                     const size_t o = (size_t)m * a.N + n;
                     const float v = acc[i][j][r] * rs;
@@ -393,7 +486,7 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
                     } else if constexpr (EPI == cwi::EPI_ADD) {
                         a.y[o] = a.resid[o] + v;
                     } else {
-                        const float up = acc[i][j + 2][r] * rs;
+                        const float up = acc[i][1][r] * rs;
                         a.y[o] = v / (1.0f + expf(-v)) * up;
                     }
                 }
@@ -708,54 +801,87 @@ int launch_split_rows(cw_ctx *ctx, const float *x, const float *norm_w, float ep
                   norm_w, eps, K, hi, lo, rowscale);
 }
 
+// Tile shape (WN waves along N) and K splits for one GEMM.  A round is one
+// workgroup per slot (two per CU); the cost of a plan is its rounds times the
+// stages each workgroup runs times WN (the MFMA work of a stage grows with
+// WN), plus, for split K, the partials' round trip through memory (S M N
+// floats written and read back, about 0.6 us of stage time per 4 MB).  Plans
+// that leave the last round part empty pay for the whole round, which is
+// what the shape choice avoids: Qwen3-8B at 512 positions runs every GEMM
+// as one full round (QKV 3 x 4 splits, O and down 2 x 4, gate/up 3 x 1).
+struct GemmPlan {
+    int wn, S, MT, NT;
+};
+
+GemmPlan gemm_plan(const cw_ctx *ctx, Epi epi, int M, int N, int K) {
+    const int MT = (M + kGM - 1) / kGM, nb = K / 32, slots = 2 * ctx->n_cu;
+    GemmPlan best{2, 1, MT, 0};
+    double best_cost = 1e30;
+    for (int wn = 2; wn <= 2; ++wn) {  // (a 2 x 3 wave tile measured slower at every shape)
+        const int bn = (epi == EPI_SWIGLU ? 32 : 64) * wn;
+        const int NT = (N + bn - 1) / bn;
+        for (int S = 1; S <= (epi == EPI_SWIGLU ? 1 : kMaxSplit); S *= 2) {
+            if (S > 1 && (nb + S - 1) / S < 16) break;  // at least 16 blocks per split
+            const long T = (long)MT * NT * S;
+            const long rounds = (T + slots - 1) / slots;
+            const int stages = ((nb + S - 1) / S + kSB - 1) / kSB;
+            const double split = S > 1 ? (double)S * M * N * 4 / (4 << 20) : 0.0;
+            const double cost = (double)rounds * stages * wn + split;
+            if (cost < best_cost - 1e-9) {
+                best_cost = cost;
+                best = GemmPlan{wn, S, MT, NT};
+            }
+        }
+    }
+    return best;
+}
+
 int gemm_splits(const cw_ctx *ctx, Epi epi, int M, int N, int K) {
-    if (epi == EPI_SWIGLU) return 1;
-    const int tiles = ((M + kGM - 1) / kGM) * ((N + kGN - 1) / kGN);
-    int s = 1;
-    // split K while the workgroups fill less than two per CU and each split
-    // keeps at least 16 blocks
-    while (s < kMaxSplit && s * tiles < 2 * ctx->n_cu && (K / 32) / (2 * s) >= 16) s *= 2;
-    return s;
+    return gemm_plan(ctx, epi, M, N, K).S;
+}
+
+size_t gemm_x_elems(int M, int K) {
+    return (size_t)((M + kGM - 1) / kGM) * kGM * K + 32;
+}
+
+template <int EPI, int OUT, int WN>
+int launch_gemm_tiles(cw_ctx *ctx, const char *label, const GemmArgs &a, const GemmPlan &p) {
+    return launch(ctx, label, q4_gemm_kernel<EPI, OUT, WN>, dim3(p.MT * p.NT * p.S),
+                  dim3(GT<WN>::THREADS), 0, a, p.MT, p.NT, p.S);
 }
 
 template <int EPI, int OUT>
-int launch_gemm_tiles(cw_ctx *ctx, const char *label, const GemmArgs &a, int MT, int NT, int S) {
-    auto fn = q4_gemm_kernel<EPI, OUT>;
-    static bool attr = false;  // per instantiation
-    if (!attr) {
-        CW_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(fn),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, 2 * kGBuf));
-        attr = true;
-    }
-    return launch(ctx, label, fn, dim3(MT * NT * S), dim3(kT), 2 * kGBuf, a, MT, NT, S);
+int launch_gemm_wn(cw_ctx *ctx, const char *label, const GemmArgs &a, const GemmPlan &p) {
+    return launch_gemm_tiles<EPI, OUT, 2>(ctx, label, a, p);
 }
 
 int launch_q4_gemm(cw_ctx *ctx, Epi epi, const GemmArgs &a) {
-    const int MT = (a.M + kGM - 1) / kGM;
-    if (epi == EPI_SWIGLU)
-        return launch_gemm_tiles<EPI_SWIGLU, 0>(ctx, "q4_gemm_swiglu", a, MT,
-                                                (a.N + kGN / 2 - 1) / (kGN / 2), 1);
-    const int NT = (a.N + kGN - 1) / kGN;
-    const int S = a.part ? gemm_splits(ctx, epi, a.M, a.N, a.K) : 1;
-    if (S > 1 && a.part_floats < (size_t)S * a.M * a.N) {
+    const GemmPlan p0 = gemm_plan(ctx, epi, a.M, a.N, a.K);
+    GemmPlan p = p0;
+    if (epi == EPI_SWIGLU) return launch_gemm_wn<EPI_SWIGLU, 0>(ctx, "q4_gemm_swiglu", a, p);
+    if (p.S > 1 && !a.part) {  // no workspace: the best unsplit plan
+        p.S = 1;
+        p.wn = 2;
+        p.NT = (a.N + 127) / 128;
+    }
+    if (p.S > 1 && a.part_floats < (size_t)p.S * a.M * a.N) {
         set_error("q4 gemm: split-K workspace of %zu floats, %zu needed", a.part_floats,
-                  (size_t)S * a.M * a.N);
+                  (size_t)p.S * a.M * a.N);
         return CW_ERR_ARG;
     }
-    if (S == 1)
-        return epi == EPI_ADD ? launch_gemm_tiles<EPI_ADD, 0>(ctx, "q4_gemm_add", a, MT, NT, 1)
-                              : launch_gemm_tiles<EPI_STORE, 0>(ctx, "q4_gemm", a, MT, NT, 1);
-    const int rc = epi == EPI_ADD
-                       ? launch_gemm_tiles<EPI_ADD, 1>(ctx, "q4_gemm_add_splitk", a, MT, NT, S)
-                       : launch_gemm_tiles<EPI_STORE, 1>(ctx, "q4_gemm_splitk", a, MT, NT, S);
+    if (p.S == 1)
+        return epi == EPI_ADD ? launch_gemm_wn<EPI_ADD, 0>(ctx, "q4_gemm_add", a, p)
+                              : launch_gemm_wn<EPI_STORE, 0>(ctx, "q4_gemm", a, p);
+    const int rc = epi == EPI_ADD ? launch_gemm_wn<EPI_ADD, 1>(ctx, "q4_gemm_add_splitk", a, p)
+                                  : launch_gemm_wn<EPI_STORE, 1>(ctx, "q4_gemm_splitk", a, p);
     if (rc != CW_OK) return rc;
     const size_t n = (size_t)a.M * a.N;
     const unsigned blocks = (unsigned)((n + 4 * kT - 1) / (4 * kT));
     if (epi == EPI_ADD)
         return launch(ctx, "q4_gemm_reduce", gemm_reduce_kernel<EPI_ADD>, dim3(blocks), dim3(kT),
-                      0, (const float *)a.part, S, n, a.resid, a.y);
+                      0, (const float *)a.part, p.S, n, a.resid, a.y);
     return launch(ctx, "q4_gemm_reduce", gemm_reduce_kernel<EPI_STORE>, dim3(blocks), dim3(kT), 0,
-                  (const float *)a.part, S, n, (const float *)nullptr, a.y);
+                  (const float *)a.part, p.S, n, (const float *)nullptr, a.y);
 }
 
 int launch_qk_rope_kv(cw_ctx *ctx, const float *qkv, const float *qn, const float *kn, float eps,
@@ -790,15 +916,17 @@ extern "C" int cw_q4_gemm(cw_ctx *ctx, const float *x, int m, const uint16_t *sc
     CW_CHECK_ARG(out_f > 0, "cw_q4_gemm: out_f=%d must be positive", out_f);
     CW_CHECK_ARG(((uintptr_t)quants & 15) == 0 && ((uintptr_t)scales & 1) == 0,
                  "cw_q4_gemm: quants must be 16-byte and scales 2-byte aligned");
-    const size_t n = (size_t)m * in_f;
+    const size_t n = gemm_x_elems(m, in_f);
     const int S = gemm_splits(ctx, EPI_STORE, m, out_f, in_f);
     const size_t part = S > 1 ? (size_t)S * m * out_f : 0;
     void *scratch = nullptr;
-    // hi, lo (2 B each per element), row scales, partials (16-byte aligned)
-    const size_t rs_off = (n * 4 + 15) & ~size_t(15);
+    // hi, lo (2 B each per element, whole row tiles), row scales, partials
+    // (16-byte aligned)
+    const size_t lo_off = (n * 2 + 15) & ~size_t(15);
+    const size_t rs_off = lo_off + ((n * 2 + 15) & ~size_t(15));
     const size_t part_off = (rs_off + (size_t)m * 4 + 15) & ~size_t(15);
     CW_TRY(ctx_scratch(ctx, part_off + part * 4, &scratch));
-    uint16_t *hi = (uint16_t *)scratch, *lo = hi + n;
+    uint16_t *hi = (uint16_t *)scratch, *lo = (uint16_t *)((char *)scratch + lo_off);
     float *rs = reinterpret_cast<float *>((char *)scratch + rs_off);
     CW_TRY(launch_split_rows(ctx, x, nullptr, 0.0f, m, in_f, hi, lo, rs));
     GemmArgs a{};

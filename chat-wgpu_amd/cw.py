@@ -110,6 +110,7 @@ _SIGS = {
     "cw_model_tap": (_I, [_P, C.c_char_p, _I, _P, _I]),
     "cw_generate": (_I, [_P, _P, _I, _I, _I, _I, _P]),
     "cw_model_decode_async": (_I, [_P, _I, _I]),
+    "cw_model_decode_next": (_I, [_P, _P]),
     "cw_model_reset_state": (_I, [_P, _U32, _I]),
     "cw_model_prefill": (_I, [_P, _P, _I, _I, C.POINTER(_U32)]),
     "cw_model_tokens": (_I, [_P, _P, _I, C.POINTER(_I)]),
@@ -617,6 +618,12 @@ class Model:
 
     def decode_async(self, n_steps, mode=STEP_GRAPH):
         check(lib().cw_model_decode_async(self.h, n_steps, int(mode)))
+
+    def decode_next(self):
+        """One replayed decode step; returns its argmax (one 4-byte read)."""
+        nxt = _U32(0)
+        check(lib().cw_model_decode_next(self.h, C.byref(nxt)))
+        return int(nxt.value)
 
     def profile_step(self):
         """One fused step with phase stamps, in microseconds from its start:

@@ -259,7 +259,7 @@ int cw_model_set_taps(cw_model *m, int enable);
  * floats; synchronises).  CW_ERR_STATE while taps are off. */
 int cw_model_tap(cw_model *m, const char *name, int layer, float *host_out, int len);
 /* How a decode step is executed (cw_generate, cw_model_decode_async). */
-#define CW_STEP_EAGER 0  /* 2 + 6*n_layers kernel launches per token */
+#define CW_STEP_EAGER 0  /* 1 + 5*n_layers kernel launches per token */
 #define CW_STEP_GRAPH 1  /* the same launches captured once as a HIP graph and replayed */
 #define CW_STEP_FUSED 2  /* one persistent cooperative kernel per token (head_dim 128) */
 
@@ -274,6 +274,11 @@ int cw_generate(cw_model *m, const uint32_t *prompt, int n_prompt, int max_new, 
 /* Launch n_steps more decode steps of the current generate state without
  * synchronising (for timing); cw_flush waits. */
 int cw_model_decode_async(cw_model *m, int n_steps, int mode);
+/* One token of the chat decode loop (src/wasm.rs:95-114: embed the last id,
+ * forward, logits, argmax): replays one CW_STEP_GRAPH step of the current
+ * decode state and returns the new argmax in *next_out with a single 4-byte
+ * read.  CW_ERR_ARG once the state's position reaches max_seq. */
+int cw_model_decode_next(cw_model *m, uint32_t *next_out);
 /* Per-phase timeline of one fused decode step (profile.rs:17-118 reports per
  * kernel; the fused step is one kernel, so it reports per phase): runs one
  * CW_STEP_FUSED step of the current generate state and writes the wall-clock
@@ -296,7 +301,6 @@ int cw_model_profile_step(cw_model *m, int64_t *ticks, int max_n, int *n_out, do
  * CW_ERR_ARG for configs the fused step does not cover. */
 int cw_step_layout_check(const cw_model_config *cfg, int n_cu, int split_gate_up, char *why,
                          size_t why_len);
-/* Reset the decode state to (token, pos) without touching the cache. */
 /* The prompt phase of model::generate (src/model/mod.rs:57-125: P forwards,
  * the logits of all but the last discarded) for n tokens at positions
  * start_pos..start_pos+n-1, batched: each layer runs as Q4_0 GEMMs on the
@@ -307,6 +311,7 @@ int cw_step_layout_check(const cw_model_config *cfg, int n_cu, int split_gate_up
  * the decode state to (next_token, start_pos + n). */
 int cw_model_prefill(cw_model *m, const uint32_t *tokens, int n, int start_pos,
                      uint32_t *next_token);
+/* Reset the decode state to (token, pos) without touching the cache. */
 int cw_model_reset_state(cw_model *m, uint32_t token, int pos);
 /* Download the tokens produced so far by the device-resident loop. */
 int cw_model_tokens(cw_model *m, uint32_t *host_out, int max_n, int *n_out);

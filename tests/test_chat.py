@@ -158,26 +158,20 @@ def test_load_tokenizer_forms(tok, tmp_path):
 
 class ScriptedDeviceLoop(ScriptedModel):
     """A stand-in that also has the device decode loop: after prefill the
-    state is (next id, position) on the "device"; decode_async(1) feeds that
-    id at that position and appends the next id to the token record."""
+    state is (next id, position) on the "device"; decode_next() feeds that
+    id at that position and returns the next id."""
 
     def prefill(self, ids):
         nxt = super().prefill(ids)
         self.state = (nxt, len(ids))
-        self.record = []
         return nxt
 
-    def decode_async(self, n_steps, mode):
-        assert mode == chat.STEP_GRAPH
-        for _ in range(n_steps):
-            token, pos = self.state
-            self.fed.append((int(token), int(pos)))
-            nxt = self._next()
-            self.record.append(nxt)
-            self.state = (nxt, pos + 1)
-
-    def tokens(self, n):
-        return self.record[:n]
+    def decode_next(self):
+        token, pos = self.state
+        self.fed.append((int(token), int(pos)))
+        nxt = self._next()
+        self.state = (nxt, pos + 1)
+        return nxt
 
     def step(self, token, pos):  # never used after a batched prompt phase
         raise AssertionError("eager step after the batched prompt phase")

@@ -348,6 +348,24 @@ def test_tensor_errors():
         cw.Gguf(data=bad_kind)
 
 
+@pytest.mark.parametrize("dtype,n", [(gw.F32, 1 << 62), (gw.F16, 1 << 63)])
+def test_byte_count_overflow_is_rejected(dtype, n):
+    """An element count whose byte size wraps 64 bits (2^62 f32 values are
+    2^64 bytes, which would read as 0) is refused before the data-section
+    range check, not passed by it."""
+    w = gw.GgufWriter()
+    w.add_tensor("huge", [n], dtype, bytes(16))
+    g = cw.Gguf(data=w.tobytes())
+    assert g.tensor_info("huge")["n_elems"] == n
+    # straight through the C entry with a small buffer: the byte range is
+    # checked before the buffer size, so nothing is written either way
+    out = np.zeros(4, np.float32)
+    rc = cw.lib().cw_gguf_tensor_f32(g.h, b"huge", out.ctypes.data_as(cw.C.c_void_p), 4)
+    assert rc == cw.CW_ERR_FORMAT
+    assert "overflow its byte count" in cw.lib().cw_last_error().decode()
+    g.close()
+
+
 def test_open_file_matches_parse(tmp_path):
     data = meta_file()
     p = tmp_path / "m.gguf"

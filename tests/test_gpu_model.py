@@ -65,6 +65,25 @@ def test_tiny_reference_model(ctx):
     m2.close()
 
 
+def test_decode_next_continues_the_prompt_phase(ctx):
+    """The chat loop's path: the prompt phase, then one replayed step per
+    token read back as its argmax (cw_model_decode_next), gives generate's
+    ids; at the last cache position it refuses with CW_ERR_ARG."""
+    import make_golden as mg
+    z = np.load(os.path.join(GOLDEN, "tiny_qwen3.npz"))
+    cfg = cw.make_config(2, 64, 4, 2, 16, 128, 256, 12, cw.CW_F32, 1e-6, 1e6)
+    m = cw.Model(ctx, cfg)
+    m.set_weights(mg.tiny_weights())
+    m.finalize()
+    got = [m.prefill(np.array([1, 5, 9, 2], np.uint32))]
+    got += [m.decode_next() for _ in range(7)]       # positions 4..10
+    assert got == [int(t) for t in z["tokens"][:8]]
+    m.decode_next()                                   # position 11, the last row
+    with pytest.raises(cw.CwError, match="at max_seq"):
+        m.decode_next()
+    m.close()
+
+
 def test_fused_step_refused_while_disabled(ctx):
     """CW_STEP_FUSED is refused with an error, never launched."""
     cfg = cw.make_config(2, 256, 4, 2, 128, 512, 1000, 8)
