@@ -198,19 +198,16 @@ struct GT {
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
 
 // One 16-byte-per-lane global -> LDS DMA: lane i's 16 bytes land at LDS byte
-// lds_off + 16 i (lds_off wave-uniform, in M0).  Written as asm so the
+// lds_off + 16 i (lds_off wave-uniform, passed in M0 through the operand
+// constraint, so the compiler sets M0 itself).  Written as asm so the
 // compiler's wait-count pass does not track it: its own waits (for register
 // loads) stay correct, being only stricter with loads it does not count, and
 // it adds none before LDS reads; the kernel orders the DMA itself with
-// counted vmcnt waits and a barrier.  M0 is written only here (the kernel has
-// no other M0 user).
+// counted vmcnt waits and a barrier.
 __device__ __forceinline__ void dma16(const void *src, unsigned char *lds_dst) {
     const uint32_t off =
         __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_u8 *)lds_dst);
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
-                 :
-                 : "v"(src), "s"(off)
-                 : "memory", "m0");
+    asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(off) : "memory");
 }
 
 __device__ __forceinline__ float f16_bits_val(uint32_t h) {
