@@ -254,19 +254,25 @@ __global__ __launch_bounds__(kThreads, 8) void q4_gemv_kernel(GemvArgs a, int n_
         if constexpr (XS == cwi::XS_RMSNORM) wn[j] = w4[ci];
     }
 
+    // the first PD groups, after the activation loads (the scheduling
+    // barriers keep that order): issued on every path (a wave with fewer
+    // groups re-reads an in-range one, unused), so the compiler's wait counts
+    // for the activation loads stay exact and staging waits for those alone
+    __builtin_amdgcn_sched_barrier(0);
     uint4 qv[PD][R];
     uint32_t dv[PD][R];
     int lk = 0, lstep = 0;  // next group to load
 #pragma unroll
     for (int u = 0; u < PD; ++u) {
-        if (u < total) {
-            load_group<G, R, EPI>(a, nb, wv + lk * stride, s + lstep * G, rl, qv[u], dv[u]);
-            if (++lstep == S) {
-                lstep = 0;
-                ++lk;
-            }
+        const bool have = u < total;
+        load_group<G, R, EPI>(a, nb, wv + lk * stride, s + (have ? lstep : 0) * G, rl, qv[u],
+                              dv[u]);
+        if (have && ++lstep == S) {
+            lstep = 0;
+            ++lk;
         }
     }
+    __builtin_amdgcn_sched_barrier(0);
 
     // ---- stage the activation in one pass: x (times the norm gain) into
     // LDS pre-scaled, with its block sums; the RMS factor 1/rms(x) is a
@@ -301,7 +307,12 @@ __global__ __launch_bounds__(kThreads, 8) void q4_gemv_kernel(GemvArgs a, int n_
         ss = group_sum<64>(ss);
         if (lane == 0) red[wave] = ss;
     }
-    __syncthreads();
+    // LDS-only barrier: a __syncthreads fence would also wait for the weight
+    // groups in flight, which staging does not read
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     float inv = 1.0f;
     if constexpr (XS == cwi::XS_RMSNORM) {
         ss = 0.0f;
