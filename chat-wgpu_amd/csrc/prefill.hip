@@ -162,6 +162,9 @@ __global__ __launch_bounds__(kT) void split_rows_kernel(const float *__restrict_
 // which global chunk each lane loads.  The block scales come through
 // registers and are stored as f32.  Each wave dequantizes its own B
 // fragments from the nibbles (perm into the f16 1024 + q, minus 1032: exact).
+// Within a block a wave issues all its LDS reads first, then interleaves the
+// previous block's scale FMAs with this block's first MFMAs, tile by tile, so
+// the vector ALU works while the matrix core runs.
 // 74 KB of LDS (two stage buffers) and at most 256 registers per lane let
 // two workgroups share a CU.
 //
@@ -293,20 +296,21 @@ __device__ __forceinline__ void nib4(uint32_t t, f16x2 &p01, f16x2 &p23) {
     p23 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, t, 0x04030402u)) - off;
 }
 
-// 8 quant bytes (w0, w1) -> B fragments (q - 8, exact in f16) of the low
-// slice (ks 0) and the high slice (ks 1)
-__device__ __forceinline__ void dequant8(uint32_t w0, uint32_t w1, f16x8 (&bq)[2]) {
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-        const uint32_t t0 = (w0 >> (4 * ks)) & 0x0F0F0F0Fu, t1 = (w1 >> (4 * ks)) & 0x0F0F0F0Fu;
-        f16x2 p[4];
-        nib4(t0, p[0], p[1]);
-        nib4(t1, p[2], p[3]);
-        bq[ks] = __builtin_bit_cast(f16x8, (u32x4){__builtin_bit_cast(uint32_t, p[0]),
-                                                   __builtin_bit_cast(uint32_t, p[1]),
-                                                   __builtin_bit_cast(uint32_t, p[2]),
-                                                   __builtin_bit_cast(uint32_t, p[3])});
-    }
+// 8 quant bytes -> the B fragment (q - 8, exact in f16) of the low slice
+// (ks 0: low nibbles) or the high slice (ks 1: high nibbles)
+__device__ __forceinline__ f16x8 dequant_slice(uint2 q, int ks) {
+    const uint32_t t0 = (q.x >> (4 * ks)) & 0x0F0F0F0Fu, t1 = (q.y >> (4 * ks)) & 0x0F0F0F0Fu;
+    f16x2 p[4];
+    nib4(t0, p[0], p[1]);
+    nib4(t1, p[2], p[3]);
+    return __builtin_bit_cast(f16x8, (u32x4){__builtin_bit_cast(uint32_t, p[0]),
+                                             __builtin_bit_cast(uint32_t, p[1]),
+                                             __builtin_bit_cast(uint32_t, p[2]),
+                                             __builtin_bit_cast(uint32_t, p[3])});
+}
+
+__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
 // Tile t of MT x NT x S -> (m tile, n tile, split), XCD-grouped when the
@@ -377,6 +381,17 @@ void q4_gemm_kernel(cwi::GemmArgs a, int MT, int NT, int S) {
     // issues the same loads (past the split's end they re-read its last
     // block, in range and unused) and the stage count is padded to even, so
     // the loop is straight-line code whose wait counts are exact.
+    // t: the current block's sums; dp: its scales.  A block's scale FMAs are
+    // issued in the next block, beside that block's first MFMAs (and after
+    // the loop for the last one); t = 0, dp = 0 make the first ones no-ops.
+    f32x16 t[2][2];
+    float dp[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) t[i][j][r] = 0.0f;
     if (n_st > 0) {
         WUnit w[2];
         auto store_w = [&](unsigned char *buf, const WUnit &u) {
@@ -409,49 +424,73 @@ void q4_gemm_kernel(cwi::GemmArgs a, int MT, int NT, int S) {
 #pragma unroll
             for (int bi = 0; bi < kSB; ++bi) {
                 if (kb + bi < kb1) {  // wave-uniform
-                    f16x8 bq[2][2];
+                    // every LDS read of the block first: the quants and scales
+                    // of both column tiles, x hi / lo of both k slices
+                    uint2 q[2];
                     float d[2];
+                    f16x8 ah[2][2], al[2][2];  // [k slice][row tile]
 #pragma unroll
                     for (int j = 0; j < 2; ++j) {
-                        const uint2 q = *reinterpret_cast<const uint2 *>(
-                            cur + G::WQ + (bi * BN + col[j]) * 16 + 8 * lg);
+                        q[j] = *reinterpret_cast<const uint2 *>(cur + G::WQ + (bi * BN + col[j]) * 16 + 8 * lg);
                         d[j] = *reinterpret_cast<const float *>(cur + G::WD + (bi * BN + col[j]) * 4);
-                        dequant8(q.x, q.y, bq[j]);
                     }
-                    // t = x . (q - 8) over the block (x_hi and x_lo, both k
-                    // slices), then acc += d t: the block scale on the f32 sum
-                    f32x16 t[2][2];
 #pragma unroll
-                    for (int ks = 0; ks < 2; ++ks) {
-                        f16x8 ah[2], al[2];
+                    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
                         for (int i = 0; i < 2; ++i) {
                             const int o = xoff(wm * 64 + i * 32 + li, bi * 4 + 2 * ks + lg);
-                            ah[i] = *reinterpret_cast<const f16x8 *>(cur + o);
-                            al[i] = *reinterpret_cast<const f16x8 *>(cur + kXHalf + o);
+                            ah[ks][i] = *reinterpret_cast<const f16x8 *>(cur + o);
+                            al[ks][i] = *reinterpret_cast<const f16x8 *>(cur + kXHalf + o);
                         }
+                    __builtin_amdgcn_sched_barrier(0);
+                    // The previous block's scale FMAs go one tile at a time,
+                    // each right before that tile's first MFMA of this block
+                    // (which overwrites the tile's sums), so they issue while
+                    // the matrix core runs the MFMA before.  The barriers pin
+                    // that order.
+                    auto scale_tile = [&](int i, int j) {
 #pragma unroll
-                        for (int i = 0; i < 2; ++i)
-#pragma unroll
-                            for (int j = 0; j < 2; ++j)
-                                t[i][j] = ks == 0 ? __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                                                        ah[i], bq[j][0], (f32x16){}, 0, 0, 0)
-                                                  : __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                                                        ah[i], bq[j][ks], t[i][j], 0, 0, 0);
-#pragma unroll
-                        for (int i = 0; i < 2; ++i)
-#pragma unroll
-                            for (int j = 0; j < 2; ++j)
-                                t[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                                    al[i], bq[j][ks], t[i][j], 0, 0, 0);
-                    }
+                        for (int r = 0; r < 16; ++r)
+                            acc[i][j][r] = __builtin_fmaf(dp[j], t[i][j][r], acc[i][j][r]);
+                    };
+                    f16x8 bq[2][2];  // [column tile][k slice]
+                    scale_tile(0, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                    bq[0][0] = dequant_slice(q[0], 0);
+                    bq[1][0] = dequant_slice(q[1], 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                    t[0][0] = mfma32(ah[0][0], bq[0][0], (f32x16){});
+                    __builtin_amdgcn_sched_barrier(0);
+                    scale_tile(0, 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                    t[0][1] = mfma32(ah[0][0], bq[1][0], (f32x16){});
+                    __builtin_amdgcn_sched_barrier(0);
+                    scale_tile(1, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                    t[1][0] = mfma32(ah[0][1], bq[0][0], (f32x16){});
+                    __builtin_amdgcn_sched_barrier(0);
+                    scale_tile(1, 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                    t[1][1] = mfma32(ah[0][1], bq[1][0], (f32x16){});
+                    __builtin_amdgcn_sched_barrier(0);
+                    // the high-nibble slice beside slice 0's x_lo MFMAs
+                    bq[0][1] = dequant_slice(q[0], 1);
+                    bq[1][1] = dequant_slice(q[1], 1);
 #pragma unroll
                     for (int i = 0; i < 2; ++i)
 #pragma unroll
-                        for (int j = 0; j < 2; ++j)
+                        for (int j = 0; j < 2; ++j) t[i][j] = mfma32(al[0][i], bq[j][0], t[i][j]);
+                    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                            for (int r = 0; r < 16; ++r)
-                                acc[i][j][r] = __builtin_fmaf(d[j], t[i][j][r], acc[i][j][r]);
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) t[i][j] = mfma32(ah[1][i], bq[j][1], t[i][j]);
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) t[i][j] = mfma32(al[1][i], bq[j][1], t[i][j]);
+                    dp[0] = d[0];
+                    dp[1] = d[1];
                 }
             }
         };
@@ -460,6 +499,12 @@ void q4_gemm_kernel(cwi::GemmArgs a, int MT, int NT, int S) {
             step(lds_b, lds_a, w[0], st + 1);
         }
     }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(dp[j], t[i][j][r], acc[i][j][r]);
 
     // lane holds rows 8 (r / 4) + 4 lg + r % 4 of each row tile, column li
     // of each column tile
@@ -576,13 +621,33 @@ __global__ __launch_bounds__(kT) void qk_rope_kv_kernel(const float *__restrict_
 // ---------------------------------------------------------------------------
 // Causal attention (attention.wgsl:23-96 for each query position) on f16
 // caches, flash style: workgroup = one query head x 64 positions, one wave
-// per 16 positions.  Per 64-key tile: K rows and V^T staged in LDS;
-// S = q K^T by MFMA (q split into f16 hi/lo), online max / sum per row,
-// P (f16 hi/lo) through LDS into A layout, O += P V by MFMA.
+// per 16 positions.  Per 64-key tile: K and V rows staged in LDS as they
+// are stored (16-byte writes); S = q K^T by MFMA (q split into f16 hi/lo),
+// online max / sum per row, P (f16 hi/lo) through LDS into A layout,
+// O += P V by MFMA with the V operand read by LDS transpose loads.
 constexpr int kAttQ = 64;   // positions per workgroup
 constexpr int kAttK = 64;   // keys per tile
-constexpr int kKRow = 128 + 8;  // K tile row stride (f16), padded
-constexpr int kVRow = kAttK + 8; // V^T tile row stride (f16), padded
+constexpr int kKRow = 128 + 8;  // K and V tile row stride (f16), padded
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// B operand of v_mfma_f32_16x16x32_f16 (lane l: B[8 (l / 16) + j][l % 16],
+// j = 0..7) from a row-major LDS tile, B[k][n] = tile[k0 + k][n0 + n].
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
+// i % 4 of the 8 bytes addressed by lane 4 j + i / 4, for j = 0..3.  So lane
+// m of group g addresses row k0 + 8 g + m / 4 (+ 4 for the second read),
+// columns n0 + 4 (m % 4) .. + 3, and lane i gets column n0 + i of rows
+// k0 + 8 g + j.
+__device__ __forceinline__ f16x8 lds_b_tr(const _Float16 *tile, int row_stride, int k0, int n0,
+                                          int lane) {
+    const int g = lane >> 4, m = lane & 15;
+    const _Float16 *p = tile + (size_t)(k0 + 8 * g + (m >> 2)) * row_stride + n0 + 4 * (m & 3);
+    const s16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)p);
+    const s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(p + 4 * row_stride));
+    const uint2 a = __builtin_bit_cast(uint2, r0), b = __builtin_bit_cast(uint2, r1);
+    return __builtin_bit_cast(f16x8, make_uint4(a.x, a.y, b.x, b.y));
+}
 
 __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
     const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)a);
@@ -597,7 +662,7 @@ __global__ __launch_bounds__(kT) void attn_prefill_kernel(const float *__restric
                                                           float scale, float *__restrict__ out) {
     constexpr int HD = 128;
     __shared__ _Float16 Ks[kAttK * kKRow];
-    __shared__ _Float16 Vt[HD * kVRow];
+    __shared__ _Float16 Vs[kAttK * kKRow];
     __shared__ float Ps[4][16 * kAttK];
     const int h = blockIdx.x, q0 = blockIdx.y * kAttQ;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -661,15 +726,13 @@ __global__ __launch_bounds__(kT) void attn_prefill_kernel(const float *__restric
     for (int t = 0; t < n_tiles; ++t) {
         const int k0 = t * kAttK;
         __syncthreads();  // previous tile's LDS reads are done
-        // stage K rows and V^T
+        // stage K and V rows
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int f = tid + u * kT;
             const int key = f >> 4, c8 = (f & 15) * 8;
             *reinterpret_cast<u32x4 *>(&Ks[key * kKRow + c8]) = kn[u];
-            const f16x8 ve = __builtin_bit_cast(f16x8, vn[u]);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) Vt[(c8 + j) * kVRow + key] = ve[j];
+            *reinterpret_cast<u32x4 *>(&Vs[key * kKRow + c8]) = vn[u];
         }
         tile_load(min(t + 1, n_tiles - 1));
         __builtin_amdgcn_sched_barrier(0);
@@ -750,8 +813,7 @@ __global__ __launch_bounds__(kT) void attn_prefill_kernel(const float *__restric
         for (int ni = 0; ni < 8; ++ni) {
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
-                const f16x8 vb = *reinterpret_cast<const f16x8 *>(
-                    &Vt[(ni * 16 + li) * kVRow + 32 * kk + 8 * lg]);
+                const f16x8 vb = lds_b_tr(Vs, kKRow, 32 * kk, ni * 16, lane);
                 o[ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[kk][0], vb, o[ni], 0, 0, 0);
                 o[ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[kk][1], vb, o[ni], 0, 0, 0);
             }
