@@ -287,6 +287,14 @@ struct GemmArgs {
     int M, N, K;
     float *part;         // split-K partials (null: no split)
     size_t part_floats;  // capacity of part
+    // optional: y also split for the next GEMM, exactly as launch_split_rows
+    // (x = y, norm_w = next_norm) would; with split K it is done by the
+    // reduction of the partials, in the same pass
+    bool split_next;
+    const float *next_norm;
+    float next_eps;
+    uint16_t *next_hi, *next_lo;
+    float *next_rowscale;
 };
 // K splits the GEMM uses for this shape (the partial workspace holds
 // splits * M * N floats)
@@ -300,10 +308,15 @@ int launch_embed_rows(cw_ctx *ctx, const float *table, int dim, const uint32_t *
                       float *out);
 int launch_split_rows(cw_ctx *ctx, const float *x, const float *norm_w, float eps, int rows, int K,
                       uint16_t *hi, uint16_t *lo, float *rowscale);
-int launch_q4_gemm(cw_ctx *ctx, Epi epi, const GemmArgs &a);
+// kept_splits (optional): with split K, leave the partials in a.part
+// unreduced and set *kept_splits = K splits (0 when y was written)
+int launch_q4_gemm(cw_ctx *ctx, Epi epi, const GemmArgs &a, int *kept_splits = nullptr);
+// qkv: [M][q | k | v] rows, or (splits > 0) the sum in order of `splits`
+// partials part[s][M][q | k | v] (gemm_reduce_kernel's sum)
 int launch_qk_rope_kv(cw_ctx *ctx, const float *qkv, const float *qn, const float *kn, float eps,
                       const float *cos_t, const float *sin_t, int M, int n_heads, int n_kv,
-                      int start, int kv_dtype, float *q_out, void *kc, void *vc);
+                      int start, int kv_dtype, float *q_out, void *kc, void *vc,
+                      const float *part = nullptr, int splits = 0);
 // causal attention of positions start..start+M-1 over an f16 cache, head_dim 128
 int launch_attn_prefill(cw_ctx *ctx, const float *q, const void *kc, const void *vc, int M,
                         int n_heads, int n_kv, int start, float *out);

@@ -513,11 +513,24 @@ int ensure_prefill(cw_model *m, int n) {
 
 // One linear layer of the batched forward: rows of x (optionally
 // RMS-normalised) through a Q4_0 matrix pair or single matrix.
+// y[n][out] = [resid +] (RMSNorm?) x . W^T on the batched GEMM.  x_split:
+// pf_hi / pf_lo / pf_rowscale already hold x's split (the previous GEMM left
+// it); next_split: leave y's split there for the next GEMM, RMS-normalised
+// with next_norm when set.
 int pf_linear(cw_model *m, const float *x, const float *norm_w, int n, int K, Epi epi,
-              const Q4W &w, const Q4W *w2, const float *resid, float *y) {
-    CW_TRY(launch_split_rows(m->ctx, x, norm_w, m->cfg.eps, n, K, m->pf_hi, m->pf_lo,
-                             m->pf_rowscale));
+              const Q4W &w, const Q4W *w2, const float *resid, float *y, bool x_split = false,
+              bool next_split = false, const float *next_norm = nullptr,
+              int *kept_splits = nullptr) {
+    if (!x_split)
+        CW_TRY(launch_split_rows(m->ctx, x, norm_w, m->cfg.eps, n, K, m->pf_hi, m->pf_lo,
+                                 m->pf_rowscale));
     GemmArgs a{};
+    a.split_next = next_split;
+    a.next_norm = next_norm;
+    a.next_eps = m->cfg.eps;
+    a.next_hi = m->pf_hi;
+    a.next_lo = m->pf_lo;
+    a.next_rowscale = m->pf_rowscale;
     a.xhi = m->pf_hi;
     a.xlo = m->pf_lo;
     a.rowscale = m->pf_rowscale;
@@ -534,7 +547,7 @@ int pf_linear(cw_model *m, const float *x, const float *norm_w, int n, int K, Ep
     a.K = K;
     a.part = m->pf_part;
     a.part_floats = m->pf_part_floats;
-    return launch_q4_gemm(m->ctx, epi, a);
+    return launch_q4_gemm(m->ctx, epi, a, kept_splits);
 }
 
 // With taps on: row `row` of a batched [n][floats] buffer into a tap.
@@ -556,20 +569,26 @@ int enqueue_prefill(cw_model *m, int n, int start) {
         Layer &L = m->layers[i];
         void *kc = (char *)m->kcache + (size_t)i * m->kv_layer_bytes;
         void *vc = (char *)m->vcache + (size_t)i * m->kv_layer_bytes;
+        // the split of the layer's input: the previous layer's down GEMM left
+        // it; with split K the partials go straight to the QK-norm + RoPE pass
+        int qkv_splits = 0;
         CW_TRY(pf_linear(m, m->pf_hidden, L.attn_norm, n, c.dim, EPI_STORE, L.qkv, nullptr,
-                         nullptr, m->pf_qkv));
+                         nullptr, m->pf_qkv, i > 0, false, nullptr, &qkv_splits));
         CW_TRY(launch_qk_rope_kv(ctx, m->pf_qkv, L.q_norm, L.k_norm, c.eps, m->cos_t, m->sin_t, n,
-                                 c.n_heads, c.n_kv_heads, start, c.kv_dtype, m->pf_q, kc, vc));
+                                 c.n_heads, c.n_kv_heads, start, c.kv_dtype, m->pf_q, kc, vc,
+                                 qkv_splits ? m->pf_part : nullptr, qkv_splits));
         CW_TRY(tap_row(m, m->tap_q + (size_t)i * m->q_dim, m->pf_q, n - 1, m->q_dim));
         CW_TRY(launch_attn_prefill(ctx, m->pf_q, kc, vc, n, c.n_heads, c.n_kv_heads, start,
                                    m->pf_attn));
         CW_TRY(pf_linear(m, m->pf_attn, nullptr, n, m->q_dim, EPI_ADD, L.wo, nullptr,
-                         m->pf_hidden, m->pf_hidden));
+                         m->pf_hidden, m->pf_hidden, false, true, L.ffn_norm));
         CW_TRY(tap_row(m, m->tap_post + (size_t)i * c.dim, m->pf_hidden, n - 1, c.dim));
         CW_TRY(pf_linear(m, m->pf_hidden, L.ffn_norm, n, c.dim, EPI_SWIGLU, L.gate, &L.up,
-                         nullptr, m->pf_act));
+                         nullptr, m->pf_act, true));
+        const bool more = i + 1 < c.n_layers;
         CW_TRY(pf_linear(m, m->pf_act, nullptr, n, c.hidden, EPI_ADD, L.down, nullptr,
-                         m->pf_hidden, m->pf_hidden));
+                         m->pf_hidden, m->pf_hidden, false, more,
+                         more ? m->layers[i + 1].attn_norm : nullptr));
         CW_TRY(tap_row(m, m->tap_out + (size_t)i * c.dim, m->pf_hidden, n - 1, c.dim));
     }
     return CW_OK;

@@ -47,22 +47,20 @@ __device__ __forceinline__ float wave_sum(float v) {
 // [2^8, 2^9): x 2^-e = hi + lo with hi = f16(.), lo = f16(remainder), and
 // rowscale[row] = 2^e restores the scale in the GEMM epilogue (exactly).
 // One workgroup per row.
+// The split of one row given the first R float4 per thread in registers
+// (xr[j], gains wr[j], element tid + j kT) and, for rows longer than R kT
+// float4, the rest read from x4 (row) and w4.
 template <bool NORM>
-__global__ __launch_bounds__(kT) void split_rows_kernel(const float *__restrict__ x,
-                                                        const float *__restrict__ w, float eps,
-                                                        int K, uint16_t *__restrict__ hi,
-                                                        uint16_t *__restrict__ lo,
-                                                        float *__restrict__ rowscale) {
-    constexpr int R = 4;  // float4 per thread held in registers (K <= 4096)
+__device__ __forceinline__ void split_row(const float4 (&xr)[4], const float4 (&wr)[4],
+                                          const float4 *x4, const float4 *w4, int K, float eps,
+                                          size_t base, uint16_t *__restrict__ hi,
+                                          uint16_t *__restrict__ lo, float *__restrict__ rowscale) {
+    constexpr int R = 4;
     __shared__ float red[2][kT / 64];
-    const size_t base = (size_t)blockIdx.x * K;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int K4 = K >> 2;
-    const float4 *x4 = reinterpret_cast<const float4 *>(x + base);
-    const float4 *w4 = reinterpret_cast<const float4 *>(w);
     // one pass for the sum of squares and max|x w| (1/rms > 0 is a common
     // factor, so max|(x/rms) w| = max|x w| / rms)
-    float4 xr[R], wr[R];
     float ss = 0.0f, mx = 0.0f;
     auto scan = [&](float4 v, float4 g) {
         if constexpr (NORM) {
@@ -74,12 +72,6 @@ __global__ __launch_bounds__(kT) void split_rows_kernel(const float *__restrict_
         }
         mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     };
-#pragma unroll
-    for (int j = 0; j < R; ++j) {
-        const int i = min(tid + j * kT, K4 - 1);
-        xr[j] = x4[i];
-        if constexpr (NORM) wr[j] = w4[i];
-    }
 #pragma unroll
     for (int j = 0; j < R; ++j)
         if (tid + j * kT < K4) scan(xr[j], NORM ? wr[j] : xr[j]);
@@ -125,6 +117,74 @@ __global__ __launch_bounds__(kT) void split_rows_kernel(const float *__restrict_
     for (int j = 0; j < R; ++j)
         if (tid + j * kT < K4) emit(tid + j * kT, xr[j], NORM ? wr[j] : xr[j]);
     for (int i = tid + R * kT; i < K4; i += kT) emit(i, x4[i], NORM ? w4[i] : x4[i]);
+}
+
+template <bool NORM>
+__global__ __launch_bounds__(kT) void split_rows_kernel(const float *__restrict__ x,
+                                                        const float *__restrict__ w, float eps,
+                                                        int K, uint16_t *__restrict__ hi,
+                                                        uint16_t *__restrict__ lo,
+                                                        float *__restrict__ rowscale) {
+    constexpr int R = 4;  // float4 per thread held in registers (K <= 4096)
+    const size_t base = (size_t)blockIdx.x * K;
+    const int tid = threadIdx.x;
+    const int K4 = K >> 2;
+    const float4 *x4 = reinterpret_cast<const float4 *>(x + base);
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+    float4 xr[R], wr[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        const int i = min(tid + j * kT, K4 - 1);
+        xr[j] = x4[i];
+        if constexpr (NORM) wr[j] = w4[i];
+    }
+    split_row<NORM>(xr, wr, x4, w4, K, eps, base, hi, lo, rowscale);
+}
+
+// The split-K reduction of one row (y = [resid +] the partials summed in
+// order, as gemm_reduce_kernel) and, in the same pass, the row's split for
+// the next GEMM (split_rows_kernel's arithmetic on y).  One workgroup per
+// row of N <= 4 kT float4.
+template <bool NORM, int EPI>
+__global__ __launch_bounds__(kT) void reduce_split_kernel(const float *__restrict__ part, int S,
+                                                          int N, size_t MN,
+                                                          const float *__restrict__ resid,
+                                                          float *__restrict__ y,
+                                                          const float *__restrict__ w, float eps,
+                                                          uint16_t *__restrict__ hi,
+                                                          uint16_t *__restrict__ lo,
+                                                          float *__restrict__ rowscale) {
+    constexpr int R = 4;
+    const size_t base = (size_t)blockIdx.x * N;
+    const int tid = threadIdx.x;
+    const int K4 = N >> 2;
+    const float4 *p4 = reinterpret_cast<const float4 *>(part + base);
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+    float4 xr[R], wr[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        const int i = min(tid + j * kT, K4 - 1);
+        float4 v = p4[i];
+        for (int s = 1; s < S; ++s) {
+            const float4 p = reinterpret_cast<const float4 *>(part + (size_t)s * MN + base)[i];
+            v.x += p.x;
+            v.y += p.y;
+            v.z += p.z;
+            v.w += p.w;
+        }
+        if constexpr (EPI == cwi::EPI_ADD) {
+            const float4 r = reinterpret_cast<const float4 *>(resid + base)[i];
+            v.x = r.x + v.x;
+            v.y = r.y + v.y;
+            v.z = r.z + v.z;
+            v.w = r.w + v.w;
+        }
+        xr[j] = v;
+        if (tid + j * kT < K4) reinterpret_cast<float4 *>(y + base)[tid + j * kT] = v;
+        if constexpr (NORM) wr[j] = w4[i];
+    }
+    split_row<NORM>(xr, wr, reinterpret_cast<const float4 *>(y + base), w4, N, eps, base, hi, lo,
+                    rowscale);
 }
 
 // ---------------------------------------------------------------------------
@@ -575,7 +635,10 @@ __global__ __launch_bounds__(kT) void gemm_reduce_kernel(const float *__restrict
 // Per position: per-head QK RMSNorm (qwen3.rs:154-155) and NeoX RoPE
 // (rope.wgsl:18-35) on the raw q|k|v rows of the QKV GEMM, q out as f32
 // [M][n_heads][hd], k and v written into the cache rows start..start+M-1
-// (cache.rs:21-24).  One workgroup per position, one wave per head (looped).
+// (cache.rs:21-24).  Workgroup (position, y) takes four heads of the
+// position, one per wave.
+// With S > 0 the rows are the QKV GEMM's S split-K partials, summed here in
+// order (gemm_reduce_kernel's sum) instead of read from qkv.
 template <typename KVT>
 __global__ __launch_bounds__(kT) void qk_rope_kv_kernel(const float *__restrict__ qkv,
                                                         const float *__restrict__ qn,
@@ -585,18 +648,27 @@ __global__ __launch_bounds__(kT) void qk_rope_kv_kernel(const float *__restrict_
                                                         int n_heads, int n_kv, int start,
                                                         float *__restrict__ q_out,
                                                         KVT *__restrict__ kc,
-                                                        KVT *__restrict__ vc) {
+                                                        KVT *__restrict__ vc,
+                                                        const float *__restrict__ part, int S,
+                                                        size_t MN) {
     constexpr int HD = 128, HALF = 64;
     const int i = blockIdx.x, pos = start + i;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int q_dim = n_heads * HD, kv_dim = n_kv * HD;
-    const float *row = qkv + (size_t)i * (q_dim + 2 * kv_dim);
+    const size_t row_off = (size_t)i * (q_dim + 2 * kv_dim);
+    const float *row = (S > 0 ? part : qkv) + row_off;
+    auto val = [&](const float *p) {  // p: an element of row (of partial 0)
+        float v = *p;
+        for (int s2 = 1; s2 < S; ++s2) v += p[(size_t)s2 * MN];
+        return v;
+    };
     const float c = cos_t[(size_t)pos * HALF + lane], s = sin_t[(size_t)pos * HALF + lane];
-    for (int h = wave; h < n_heads + n_kv; h += kT / 64) {
+    // one head per wave: workgroup y takes heads 4 y .. 4 y + 3 of the row
+    for (int h = blockIdx.y * (kT / 64) + wave; h < n_heads + n_kv; h += gridDim.y * (kT / 64)) {
         const bool isq = h < n_heads;
         const float *src = isq ? row + (size_t)h * HD : row + q_dim + (size_t)(h - n_heads) * HD;
         const float *g = isq ? qn : kn;
-        const float lo = src[lane], hi = src[lane + HALF];
+        const float lo = val(src + lane), hi = val(src + lane + HALF);
         const float ss = wave_sum(lo * lo + hi * hi);
         const float inv = 1.0f / sqrtf(ss / (float)HD + eps);
         const float l0 = (lo * inv) * g[lane], h0 = (hi * inv) * g[lane + HALF];
@@ -612,8 +684,8 @@ __global__ __launch_bounds__(kT) void qk_rope_kv_kernel(const float *__restrict_
             kd[lane + HALF] = (KVT)r1;
             const float *vs = row + q_dim + kv_dim + (size_t)g2 * HD;
             KVT *vd = vc + (size_t)pos * kv_dim + (size_t)g2 * HD;
-            vd[lane] = (KVT)vs[lane];
-            vd[lane + HALF] = (KVT)vs[lane + HALF];
+            vd[lane] = (KVT)val(vs + lane);
+            vd[lane + HALF] = (KVT)val(vs + lane + HALF);
         }
     }
 }
@@ -914,10 +986,34 @@ int launch_gemm_wn(cw_ctx *ctx, const char *label, const GemmArgs &a, const Gemm
     return launch_gemm_tiles<EPI, OUT, 2>(ctx, label, a, p);
 }
 
-int launch_q4_gemm(cw_ctx *ctx, Epi epi, const GemmArgs &a) {
+// y split for the next GEMM after the GEMM wrote it
+int split_next(cw_ctx *ctx, const GemmArgs &a) {
+    if (!a.split_next) return CW_OK;
+    return launch_split_rows(ctx, a.y, a.next_norm, a.next_eps, a.M, a.N, a.next_hi, a.next_lo,
+                             a.next_rowscale);
+}
+
+template <int EPI>
+int launch_reduce_split(cw_ctx *ctx, const GemmArgs &a, int S) {
+    const size_t mn = (size_t)a.M * a.N;
+    if (a.next_norm)
+        return launch(ctx, "q4_gemm_reduce_split", reduce_split_kernel<true, EPI>, dim3(a.M),
+                      dim3(kT), 0, (const float *)a.part, S, a.N, mn, a.resid, a.y, a.next_norm,
+                      a.next_eps, a.next_hi, a.next_lo, a.next_rowscale);
+    return launch(ctx, "q4_gemm_reduce_split", reduce_split_kernel<false, EPI>, dim3(a.M), dim3(kT),
+                  0, (const float *)a.part, S, a.N, mn, a.resid, a.y, a.next_norm, a.next_eps,
+                  a.next_hi, a.next_lo, a.next_rowscale);
+}
+
+int launch_q4_gemm(cw_ctx *ctx, Epi epi, const GemmArgs &a, int *kept_splits) {
+    if (kept_splits) *kept_splits = 0;
     const GemmPlan p0 = gemm_plan(ctx, epi, a.M, a.N, a.K);
     GemmPlan p = p0;
-    if (epi == EPI_SWIGLU) return launch_gemm_wn<EPI_SWIGLU, 0>(ctx, "q4_gemm_swiglu", a, p);
+    if (epi == EPI_SWIGLU) {
+        const int rc = launch_gemm_wn<EPI_SWIGLU, 0>(ctx, "q4_gemm_swiglu", a, p);
+        if (rc != CW_OK) return rc;
+        return split_next(ctx, a);
+    }
     if (p.S > 1 && !a.part) {  // no workspace: the best unsplit plan
         p.S = 1;
         p.wn = 2;
@@ -928,30 +1024,52 @@ int launch_q4_gemm(cw_ctx *ctx, Epi epi, const GemmArgs &a) {
                   (size_t)p.S * a.M * a.N);
         return CW_ERR_ARG;
     }
-    if (p.S == 1)
-        return epi == EPI_ADD ? launch_gemm_wn<EPI_ADD, 0>(ctx, "q4_gemm_add", a, p)
-                              : launch_gemm_wn<EPI_STORE, 0>(ctx, "q4_gemm", a, p);
+    if (p.S == 1) {
+        const int rc = epi == EPI_ADD ? launch_gemm_wn<EPI_ADD, 0>(ctx, "q4_gemm_add", a, p)
+                                      : launch_gemm_wn<EPI_STORE, 0>(ctx, "q4_gemm", a, p);
+        if (rc != CW_OK) return rc;
+        return split_next(ctx, a);
+    }
     const int rc = epi == EPI_ADD ? launch_gemm_wn<EPI_ADD, 1>(ctx, "q4_gemm_add_splitk", a, p)
                                   : launch_gemm_wn<EPI_STORE, 1>(ctx, "q4_gemm_splitk", a, p);
     if (rc != CW_OK) return rc;
+    if (kept_splits) {  // the caller reduces the partials itself
+        *kept_splits = p.S;
+        return CW_OK;
+    }
+    // the reduction and the next split in one pass when a row fits one
+    // workgroup's registers (float4 rows, 16-byte aligned)
+    const bool aligned = ((reinterpret_cast<uintptr_t>(a.y) | reinterpret_cast<uintptr_t>(a.resid) |
+                           reinterpret_cast<uintptr_t>(a.part)) & 15) == 0;
+    if (a.split_next && a.N % 4 == 0 && a.N / 4 <= 4 * kT && aligned)
+        return epi == EPI_ADD ? launch_reduce_split<EPI_ADD>(ctx, a, p.S)
+                              : launch_reduce_split<EPI_STORE>(ctx, a, p.S);
     const size_t n = (size_t)a.M * a.N;
     const unsigned blocks = (unsigned)((n + 4 * kT - 1) / (4 * kT));
-    if (epi == EPI_ADD)
-        return launch(ctx, "q4_gemm_reduce", gemm_reduce_kernel<EPI_ADD>, dim3(blocks), dim3(kT),
-                      0, (const float *)a.part, p.S, n, a.resid, a.y);
-    return launch(ctx, "q4_gemm_reduce", gemm_reduce_kernel<EPI_STORE>, dim3(blocks), dim3(kT), 0,
-                  (const float *)a.part, p.S, n, (const float *)nullptr, a.y);
+    const int rr =
+        epi == EPI_ADD
+            ? launch(ctx, "q4_gemm_reduce", gemm_reduce_kernel<EPI_ADD>, dim3(blocks), dim3(kT), 0,
+                     (const float *)a.part, p.S, n, a.resid, a.y)
+            : launch(ctx, "q4_gemm_reduce", gemm_reduce_kernel<EPI_STORE>, dim3(blocks), dim3(kT),
+                     0, (const float *)a.part, p.S, n, (const float *)nullptr, a.y);
+    if (rr != CW_OK) return rr;
+    return split_next(ctx, a);
 }
 
 int launch_qk_rope_kv(cw_ctx *ctx, const float *qkv, const float *qn, const float *kn, float eps,
                       const float *cos_t, const float *sin_t, int M, int n_heads, int n_kv,
-                      int start, int kv_dtype, float *q_out, void *kc, void *vc) {
+                      int start, int kv_dtype, float *q_out, void *kc, void *vc, const float *part,
+                      int splits) {
+    const size_t mn = (size_t)M * (n_heads + 2 * n_kv) * 128;
+    const int S = part ? splits : 0;
+    const dim3 grid(M, (n_heads + n_kv + kT / 64 - 1) / (kT / 64));
     if (kv_dtype == CW_F16)
-        return launch(ctx, "prefill_qk_rope_kv", qk_rope_kv_kernel<_Float16>, dim3(M), dim3(kT), 0,
+        return launch(ctx, "prefill_qk_rope_kv", qk_rope_kv_kernel<_Float16>, grid, dim3(kT), 0,
                       qkv, qn, kn, eps, cos_t, sin_t, n_heads, n_kv, start, q_out, (_Float16 *)kc,
-                      (_Float16 *)vc);
-    return launch(ctx, "prefill_qk_rope_kv", qk_rope_kv_kernel<float>, dim3(M), dim3(kT), 0, qkv,
-                  qn, kn, eps, cos_t, sin_t, n_heads, n_kv, start, q_out, (float *)kc, (float *)vc);
+                      (_Float16 *)vc, part, S, mn);
+    return launch(ctx, "prefill_qk_rope_kv", qk_rope_kv_kernel<float>, grid, dim3(kT), 0, qkv,
+                  qn, kn, eps, cos_t, sin_t, n_heads, n_kv, start, q_out, (float *)kc, (float *)vc,
+                  part, S, mn);
 }
 
 int launch_attn_prefill(cw_ctx *ctx, const float *q, const void *kc, const void *vc, int M,
