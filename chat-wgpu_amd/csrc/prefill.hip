@@ -692,11 +692,14 @@ __global__ __launch_bounds__(kT) void qk_rope_kv_kernel(const float *__restrict_
 
 // ---------------------------------------------------------------------------
 // Causal attention (attention.wgsl:23-96 for each query position) on f16
-// caches, flash style: workgroup = one query head x 64 positions, one wave
-// per 16 positions.  Per 64-key tile: K and V rows staged in LDS as they
-// are stored (16-byte writes); S = q K^T by MFMA (q split into f16 hi/lo),
-// online max / sum per row, P (f16 hi/lo) through LDS into A layout,
-// O += P V by MFMA with the V operand read by LDS transpose loads.
+// caches, flash style: workgroup = one query head x 64 positions, in two
+// groups of four waves (one wave per 16 positions) that take alternate
+// 64-key tiles, so the longest workgroup runs half as many tile steps.  Per
+// tile: K and V rows staged in LDS as they are stored (16-byte writes);
+// S = q K^T by MFMA (q split into f16 hi/lo), online max / sum per row,
+// P (f16 hi/lo) through LDS into A layout, O += P V by MFMA with the V
+// operand read by LDS transpose loads.  At the end the second group's
+// (max, sum, o) per row merges into the first's through LDS.
 constexpr int kAttQ = 64;   // positions per workgroup
 constexpr int kAttK = 64;   // keys per tile
 constexpr int kKRow = 128 + 8;  // K and V tile row stride (f16), padded
@@ -727,22 +730,25 @@ __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
     return lo | (hi << 16);
 }
 
-__global__ __launch_bounds__(kT) void attn_prefill_kernel(const float *__restrict__ q,
-                                                          const _Float16 *__restrict__ kc,
-                                                          const _Float16 *__restrict__ vc,
-                                                          int M, int n_heads, int n_kv, int start,
-                                                          float scale, float *__restrict__ out) {
+constexpr int kAttThreads = 2 * kT;  // two groups of four waves
+
+__global__ __launch_bounds__(kAttThreads) void attn_prefill_kernel(
+    const float *__restrict__ q, const _Float16 *__restrict__ kc, const _Float16 *__restrict__ vc,
+    int M, int n_heads, int n_kv, int start, float scale, float *__restrict__ out) {
     constexpr int HD = 128;
-    __shared__ _Float16 Ks[kAttK * kKRow];
-    __shared__ _Float16 Vs[kAttK * kKRow];
-    __shared__ float Ps[4][16 * kAttK];
+    constexpr int TILE = kAttK * kKRow;  // f16 elements of one K (or V) tile
+    // [group][K | V]; after the loop, group 1's (o, m, l) for the merge
+    __shared__ __attribute__((aligned(16))) _Float16 KV[2][2][TILE];
+    __shared__ float Ps[8][16 * kAttK];
     const int h = blockIdx.x, q0 = blockIdx.y * kAttQ;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave >> 2, gw = wave & 3, gtid = tid & (kT - 1);
     const int li = lane & 15, lg = lane >> 4;
     const int g = h / (n_heads / n_kv);
     const int kv_dim = n_kv * HD;
-    const int wq = q0 + wave * 16;  // this wave's first position (row of q)
+    const int wq = q0 + gw * 16;  // this wave's first position (row of q)
+    _Float16 *Ks = KV[grp][0], *Vs = KV[grp][1];
 
     // q operands: row li of the wave's 16, dims 8 lg + 32 ks .. +8, hi and lo
     f16x8 qa[4][2];
@@ -780,35 +786,39 @@ __global__ __launch_bounds__(kT) void attn_prefill_kernel(const float *__restric
 
     const int last_pos = start + min(q0 + kAttQ, M) - 1;  // last key any row needs
     const int n_tiles = last_pos / kAttK + 1;
+    const int n_steps = (n_tiles + 1) / 2;  // group grp takes tiles grp, grp + 2, ...
     // K and V rows of key tile t, 64 keys x 128 dims, 16 B per load (4 each
-    // per thread); the next tile's loads are in flight during this tile's
-    // MFMAs (past the last tile a clamped re-load, unused)
+    // per thread of the group); the group's next tile's loads are in flight
+    // during this tile's MFMAs (past the last tile a clamped re-load, unused)
     u32x4 kn[4], vn[4];
     auto tile_load = [&](int t) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int f = tid + u * kT;  // 0..1023
+            const int f = gtid + u * kT;  // 0..1023
             const int key = f >> 4, c8 = (f & 15) * 8;
             const int p = min(t * kAttK + key, last_pos);
             kn[u] = *reinterpret_cast<const u32x4 *>(kc + (size_t)p * kv_dim + g * HD + c8);
             vn[u] = *reinterpret_cast<const u32x4 *>(vc + (size_t)p * kv_dim + g * HD + c8);
         }
     };
-    tile_load(0);
-    for (int t = 0; t < n_tiles; ++t) {
+    tile_load(min(grp, n_tiles - 1));
+    for (int st = 0; st < n_steps; ++st) {
+        const int t = 2 * st + grp;
+        const bool active = t < n_tiles;  // (uniform over the group)
         const int k0 = t * kAttK;
-        __syncthreads();  // previous tile's LDS reads are done
+        __syncthreads();  // previous step's LDS reads are done
         // stage K and V rows
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int f = tid + u * kT;
+            const int f = gtid + u * kT;
             const int key = f >> 4, c8 = (f & 15) * 8;
             *reinterpret_cast<u32x4 *>(&Ks[key * kKRow + c8]) = kn[u];
             *reinterpret_cast<u32x4 *>(&Vs[key * kKRow + c8]) = vn[u];
         }
-        tile_load(min(t + 1, n_tiles - 1));
+        tile_load(min(t + 2, n_tiles - 1));
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
+        if (!active) continue;
 
         // S (16 rows x 64 keys): 4 key tiles of 16, K = 128 dims in 4 steps
         f32x4 sc[4];
@@ -841,7 +851,7 @@ __global__ __launch_bounds__(kT) void attn_prefill_kernel(const float *__restric
 #pragma unroll
             for (int off = 8; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
             const float mnew = fmaxf(mrow[r], mx);
-            // a row with no key yet in this tile keeps mnew = -inf: guard the rescale
+            // a row with no key yet keeps mnew = -inf: guard the rescale
             const float alpha = mnew == -INFINITY ? 1.0f : expf(mrow[r] - mnew);
             float ls = 0.0f;
 #pragma unroll
@@ -891,15 +901,43 @@ __global__ __launch_bounds__(kT) void attn_prefill_kernel(const float *__restric
             }
         }
     }
-    // normalise and store: lane holds rows 4 lg + r, dims ni * 16 + li
+
+    // merge: group 1's (o, m, l) of each row through LDS into group 0's
+    // (rescaled to the common max), then normalise and store.  Lane holds
+    // rows 4 lg + r, dims ni * 16 + li.
+    __syncthreads();  // every group is done with its K / V tile
+    float *mo = reinterpret_cast<float *>(&KV[0][0][0]);  // [4 waves][16 rows][128]
+    float *mml = mo + 4 * 16 * HD;                        // [4 waves][16 rows][2]
+    if (grp == 1) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int qi = wq + 4 * lg + r;
-        if (qi < M) {
-            const float inv = 1.0f / lrow[r];
-            float *dst = out + (size_t)qi * n_heads * HD + (size_t)h * HD;
+        for (int r = 0; r < 4; ++r) {
+            const int row = 4 * lg + r;
 #pragma unroll
-            for (int ni = 0; ni < 8; ++ni) dst[ni * 16 + li] = o[ni][r] * inv;
+            for (int ni = 0; ni < 8; ++ni) mo[(gw * 16 + row) * HD + ni * 16 + li] = o[ni][r];
+            if (li == 0) {
+                mml[(gw * 16 + row) * 2] = mrow[r];
+                mml[(gw * 16 + row) * 2 + 1] = lrow[r];
+            }
+        }
+    }
+    __syncthreads();
+    if (grp == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 4 * lg + r;
+            const int qi = wq + row;
+            const float m1 = mml[(gw * 16 + row) * 2], l1 = mml[(gw * 16 + row) * 2 + 1];
+            const float mm = fmaxf(mrow[r], m1);
+            const float f0 = mrow[r] == -INFINITY ? 0.0f : expf(mrow[r] - mm);
+            const float f1 = m1 == -INFINITY ? 0.0f : expf(m1 - mm);
+            const float inv = 1.0f / (lrow[r] * f0 + l1 * f1);
+            if (qi < M) {
+                float *dst = out + (size_t)qi * n_heads * HD + (size_t)h * HD;
+#pragma unroll
+                for (int ni = 0; ni < 8; ++ni)
+                    dst[ni * 16 + li] =
+                        (o[ni][r] * f0 + mo[(gw * 16 + row) * HD + ni * 16 + li] * f1) * inv;
+            }
         }
     }
 }
@@ -1076,7 +1114,7 @@ int launch_attn_prefill(cw_ctx *ctx, const float *q, const void *kc, const void 
                         int n_heads, int n_kv, int start, float *out) {
     const float scale = 1.0f / sqrtf(128.0f);
     return launch(ctx, "prefill_attention", attn_prefill_kernel,
-                  dim3(n_heads, (M + kAttQ - 1) / kAttQ), dim3(kT), 0, q,
+                  dim3(n_heads, (M + kAttQ - 1) / kAttQ), dim3(kAttThreads), 0, q,
                   (const _Float16 *)kc, (const _Float16 *)vc, M, n_heads, n_kv, start, scale, out);
 }
 
