@@ -789,14 +789,14 @@ int cw_model_set_q4(cw_model *m, const char *name, const uint16_t *scales, const
     Layer &L = m->layers[li];
     int out_f = 0, in_f = 0;
     proj_shape(m, id, &out_f, &in_f);
-    // the batched prefill holds each weight (q - 8) d exactly as two f16
-    // parts, which needs |d| < 8192 (|weight| < 65536; real weights are far
-    // smaller); NaN and infinite scales are refused too
+    // NaN and infinite block scales are refused: the batched prefill
+    // multiplies each block's f32 sum by d, where the per-token path forms
+    // d (q - 8) per weight, and the two agree for every finite d only
     const size_t nblk = (size_t)out_f * (in_f / 32);
     for (size_t b = 0; b < nblk; ++b)
-        CW_CHECK_ARG((scales[b] & 0x7FFFu) < 0x7000u,
-                     "cw_model_set_q4: %s block %zu has scale bits 0x%04x (|d| >= 8192 or not "
-                     "finite)", name, b, (unsigned)scales[b]);
+        CW_CHECK_ARG((scales[b] & 0x7C00u) != 0x7C00u,
+                     "cw_model_set_q4: %s block %zu has scale bits 0x%04x (not finite)", name, b,
+                     (unsigned)scales[b]);
     switch (id) {
         case T_Q: CW_TRY(upload_rows(m, L.qkv, 0, out_f, scales, quants)); break;
         case T_K: CW_TRY(upload_rows(m, L.qkv, m->q_dim, out_f, scales, quants)); break;

@@ -165,7 +165,7 @@ int cw_hbm_read_probe(cw_ctx *ctx, const void *buf, size_t bytes, int blocks, ui
  * . W^T for m rows at once, on the matrix cores (the reference has no batched
  * path; every row equals cw_q4_gemv of that row to within 1e-4 relative).
  * x and y device f32, row-major; quants 16-byte aligned; block scales must be
- * finite with |d| < 8192 (weights are held as exact f16 parts). */
+ * finite (each block's f32 sum is multiplied by its scale). */
 int cw_q4_gemm(cw_ctx *ctx, const float *x, int m, const uint16_t *scales, const uint8_t *quants,
                int in_f, int out_f, float *y);
 
@@ -225,7 +225,7 @@ int cw_model_create(cw_ctx *ctx, const cw_model_config *cfg, cw_model **out);
 int cw_model_destroy(cw_model *m);
 /* Weights::matrix_raw + Q4Linear (src/model/mod.rs:130-153, layers.rs:74-95),
  * by GGUF name ("blk.3.attn_q.weight", "output.weight", ...).  Layer
- * projections need block scales |d| < 8192 (finite): CW_ERR_ARG otherwise. */
+ * projections need finite block scales: CW_ERR_ARG otherwise. */
 int cw_model_set_q4(cw_model *m, const char *name, const uint16_t *scales_host,
                     const uint8_t *quants_host);
 /* Weights::vector (norm gains "blk.3.attn_norm.weight", "output_norm.weight";

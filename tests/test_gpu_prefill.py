@@ -92,6 +92,26 @@ def test_q4_gemm_rows_match_gemv(ctx):
         assert rel_err(y[i], g.astype(np.float64)) <= 1e-4, i
 
 
+def test_q4_gemm_large_scales(ctx):
+    """Block scales up to the f16 maximum (and the smallest subnormal) go
+    through the GEMM as they do through the oracle's GEMV: each block's f32
+    sum times d."""
+    m, in_f, out_f = 37, 512, 96
+    s, q = cw.synth_q4(cw.synth_key(24, "w"), out_f, in_f, 0.02)
+    big = np.array([8192.0, -30000.0, 65504.0, -65504.0, 2.0 ** -24], np.float16).view(np.uint16)
+    rng = np.random.default_rng(24)
+    pick = rng.integers(0, s.size, 200)
+    s.reshape(-1)[pick] = big[np.arange(200) % big.size]
+    x = cw.synth_normal_f32(cw.synth_key(24, "x"), m * in_f).reshape(m, in_f)
+    y = ctx.q4_gemm(ctx.storage(x), m, ctx.storage(s), ctx.storage(q), in_f, out_f).download()
+    y = y.reshape(m, out_f)
+    assert np.all(np.isfinite(y))
+    for i in range(m):
+        y64, absy = orc.q4_gemv_f64(x[i], s, q, in_f, out_f)
+        assert np.all(np.abs(y[i] - y64) <= 2e-5 * absy + 1e-30), i
+        assert rel_err(y[i], orc.q4_gemv(x[i], s, q, in_f, out_f)) <= 1e-4, i
+
+
 def test_q4_gemm_argument_errors(ctx):
     s, q = cw.synth_q4(cw.synth_key(1, "e"), 64, 64, 0.02)
     x = ctx.storage(np.zeros((2, 64), np.float32))
@@ -102,17 +122,21 @@ def test_q4_gemm_argument_errors(ctx):
         ctx.q4_gemm(x, 0, sd, qd, 64, 64)   # no rows
 
 
-def test_model_rejects_out_of_range_scales(ctx):
-    """A projection block scale |d| >= 8192 (or not finite) is refused at
-    upload: the batched GEMM holds each weight as exact f16 parts."""
+def test_model_rejects_non_finite_scales(ctx):
+    """A projection block scale that is not finite is refused at upload;
+    large finite ones (8192, the f16 maximum) are accepted."""
     cfg = cw.make_config(1, 64, 2, 1, 32, 64, 100, 8, cw.CW_F16)
     m = cw.Model(ctx, cfg)
     s, q = cw.synth_q4(cw.synth_key(3, "w"), 64, 64, 0.02)
-    for bad in (0x7000, 0xF000, 0x7C00, 0x7E00):   # 8192, -8192, inf, NaN
+    for bad in (0x7C00, 0xFC00, 0x7E00, 0xFE01):   # +inf, -inf, NaNs
         s2 = s.copy()
         s2[5, 1] = bad
         with pytest.raises(cw.CwError, match="block 11"):
             m.set_weights({"blk.0.attn_q.weight": (s2, q)})
+    for big in (0x7000, 0xF000, 0x7BFF):   # 8192, -8192, 65504
+        s2 = s.copy()
+        s2[5, 1] = big
+        m.set_weights({"blk.0.attn_q.weight": (s2, q)})
     m.set_weights({"blk.0.attn_q.weight": (s, q)})
     m.close()
 
