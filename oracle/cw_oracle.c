@@ -33,7 +33,12 @@
  *   or_swiglu / or_add     main.rs:77-82 and main.rs:154-161 KATs
  *   or_argmax              argmax.wgsl:4-5,43 tie rule, brute force
  *   or_fill / or_fnv_seed  main.rs:253-266 ([-0.1, 0) range quirk)
- *   model forward          composition of the above; qwen3.rs:139-191
+ *   model forward          qwen3.rs:139-191: closed-form composition checks
+ *   and generate           (tests/test_oracle_composition.py: attention and
+ *                          FFN switched off, pos 0 -> V under the GQA map,
+ *                          the K row written, zero query -> mean of V, the
+ *                          FFN alone, P + N - 1 forwards) and the tiny-model
+ *                          fixture; mod.rs:57-125
  */
 #include <math.h>
 #include <omp.h>
