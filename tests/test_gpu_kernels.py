@@ -257,6 +257,9 @@ ATTN_CASES = [  # (n_heads, n_kv, hd, seq, f16)
     (32, 8, 128, 9000, False),
     # f16 cache past one merge round (94 chunks of 128 positions)
     (32, 8, 128, 12000, True),
+    # the f16 head_dim-128 kernel with one query head per kv head, and with
+    # eight per kv head over two kv heads
+    (8, 8, 128, 777, True), (16, 2, 128, 513, True),
 ]
 
 
