@@ -65,6 +65,29 @@ def test_tiny_reference_model(ctx):
     m2.close()
 
 
+@pytest.mark.parametrize("n_heads,n_kv", [(4, 4), (8, 1), (16, 2)])
+def test_f16_head128_query_groupings(ctx, n_heads, n_kv):
+    """Decode with the f16 head_dim-128 attention fused into the step (QK-norm,
+    RoPE and the KV write in its prologue) for one and for eight query heads
+    per kv head: greedy ids identical to the oracle's over a 6-token prompt
+    and 16 produced tokens, teacher-forced logits within 1e-3."""
+    cfg = cw.make_config(2, 256, n_heads, n_kv, 128, 512, 1000, 40, cw.CW_F16, 1e-6, 1e6)
+    weights = cw.synthetic_weights(cfg, 90 + n_heads + n_kv)
+    prompt = cw.synth_tokens(cw.synth_key(91, f"g{n_heads}x{n_kv}"), 6, cfg.vocab)
+    m, o = build_pair(ctx, cfg, weights)
+    toks = m.generate(prompt, 16, mode=cw.STEP_GRAPH)
+    ref, margins = o.generate(prompt, 16)
+    first_diff = np.nonzero(toks != ref)[0]
+    msg = "" if not first_diff.size else (
+        f"first divergence at step {first_diff[0]}: margin {margins[first_diff[0]]:.3e}")
+    assert np.array_equal(toks, ref), msg
+    m2, o2 = build_pair(ctx, cfg, weights)
+    worst = teacher_forced(m2, o2, list(prompt) + list(ref[:10]))
+    print(f"\n[{n_heads}/{n_kv} heads] max |logit diff| = {worst:.3e}", flush=True)
+    for x in (m, o, m2, o2):
+        x.close()
+
+
 def test_decode_next_continues_the_prompt_phase(ctx):
     """The chat loop's path: the prompt phase, then one replayed step per
     token read back as its argmax (cw_model_decode_next), gives generate's
