@@ -180,6 +180,34 @@ def test_prefill_small_model(ctx, P):
     o.close()
 
 
+@pytest.mark.parametrize("n_heads,n_kv", [(4, 4), (8, 1), (16, 2)])
+def test_prefill_query_groupings(ctx, n_heads, n_kv):
+    """The batched prompt phase (130 positions: two whole 64-position tiles
+    and a ragged one) with one and with eight query heads per kv head: last
+    position's logits within 1e-3 of the oracle's per-token forward, the same
+    next token, then 8 greedy decode steps from the prefilled cache."""
+    P, N = 130, 8
+    cfg = small_f16(P + N + 1, n_heads=n_heads, n_kv=n_kv)
+    weights = cw.synthetic_weights(cfg, 78 + n_heads + n_kv)
+    prompt = cw.synth_tokens(cw.synth_key(78, f"q{n_heads}x{n_kv}"), P, cfg.vocab)
+    m = cw.Model(ctx, cfg)
+    m.set_weights(weights)
+    m.finalize()
+    o = orc.OracleModel(cfg, weights)
+    nxt = m.prefill(prompt)
+    ref_logits = oracle_prompt_logits(o, prompt)
+    diff = float(np.max(np.abs(m.logits() - ref_logits)))
+    assert diff <= LOGIT_TOL, diff
+    assert nxt == int(np.argmax(ref_logits))
+    m.decode_async(N, mode=cw.STEP_GRAPH)
+    toks = m.tokens(N)
+    ref, _ = o.generate(prompt, N + 1)
+    assert int(ref[0]) == nxt
+    assert np.array_equal(toks, ref[1:N + 1]), (toks, ref[1:N + 1])
+    m.close()
+    o.close()
+
+
 def test_prefill_in_chunks_equals_one_pass(ctx):
     """Two prefill calls (positions 0..39, then 40..99 over the cache the
     first wrote) leave the same logits and next token as one 100-position
