@@ -260,6 +260,8 @@ ATTN_CASES = [  # (n_heads, n_kv, hd, seq, f16)
     # the f16 head_dim-128 kernel with one query head per kv head, and with
     # eight per kv head over two kv heads
     (8, 8, 128, 777, True), (16, 2, 128, 513, True),
+    # the f32 head_dim-128 kernel at the same groupings
+    (8, 8, 128, 300, False), (8, 1, 128, 200, False),
 ]
 
 
