@@ -16,6 +16,7 @@ CPU oracle baseline on a bounded sample, and the Qwen3-0.6B-shape token loop.
   python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
 import argparse
+import contextlib
 import json
 import os
 import platform
@@ -83,24 +84,40 @@ def step_bytes(cfg, seq, es):
     return w + kv_rw + small, w
 
 
+@contextlib.contextmanager
+def pinned_core():
+    """Run the calling thread (the one-thread oracle runs on it) on one core,
+    the lowest this process may use (core 0 when allowed), as `taskset -c 0`
+    would; yields that core and restores the previous affinity."""
+    old = os.sched_getaffinity(0)
+    core = 0 if 0 in old else min(old)
+    os.sched_setaffinity(0, {core})
+    try:
+        yield core
+    finally:
+        os.sched_setaffinity(0, old)
+
+
 def cpu_baseline_8b(cfg, weights, k, v, start_tok, budget_s):
-    """The CPU oracle (C restatement of the reference forward, single thread)
-    on decode tokens from position 4096 until budget_s has elapsed."""
+    """The CPU oracle (C restatement of the reference forward, single thread
+    pinned to one core) on decode tokens from position 4096 until budget_s
+    has elapsed.  Returns (tokens/s, tokens, seconds, core)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
     orc.set_threads(1)
     o = orc.OracleModel(cfg, weights)
     o.prefill_kv(k, v, PRE)
-    tok, n, t0 = int(start_tok), 0, time.perf_counter()
-    while True:
-        logits, _ = o.step(tok, PRE + n)
-        tok = int(np.argmax(logits))
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or n >= 8:
-            break
+    with pinned_core() as core:
+        tok, n, t0 = int(start_tok), 0, time.perf_counter()
+        while True:
+            logits, _ = o.step(tok, PRE + n)
+            tok = int(np.argmax(logits))
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s or n >= 8:
+                break
     o.close()
-    return n / el, n, el
+    return n / el, n, el, core
 
 
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16 matrix peak
@@ -255,8 +272,9 @@ def cpu_single_gemv(out_f=3072, in_f=1024, budget_s=1.0):
             el = time.perf_counter() - t0
             if el >= budget_s:
                 return el / n * 1e6
-    t_q4 = timed(lambda: orc.q4_gemv(x, s, q, in_f, out_f))
-    t_nm = timed(lambda: orc.naive_matmul(x, wt, 1, in_f, out_f))
+    with pinned_core():
+        t_q4 = timed(lambda: orc.q4_gemv(x, s, q, in_f, out_f))
+        t_nm = timed(lambda: orc.naive_matmul(x, wt, 1, in_f, out_f))
     return t_q4, t_nm
 
 
@@ -410,13 +428,14 @@ def main():
 
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle, 1 thread) ...")
-        tps, n, cel = cpu_baseline_8b(cfg, weights, k, v, start, args.cpu_budget)
+        tps, n, cel, core = cpu_baseline_8b(cfg, weights, k, v, start, args.cpu_budget)
         model_name, ncpu = cpu_info()
         result["cpu_baseline"] = {"value": round(tps, 5), "unit": "tokens/s", "cores": 1,
                                   "kind": "port",
                                   "sample": f"{n} decode tokens of the same 8B workload from "
-                                            f"position 4096 on the C oracle ({cel:.1f}s); "
-                                            f"host {model_name}, {ncpu} cpus"}
+                                            f"position 4096 on the C oracle ({cel:.1f}s), one "
+                                            f"thread pinned to cpu {core}; host {model_name}, "
+                                            f"{ncpu} cpus"}
     del weights
     if not args.no_extras:
         log("prefill (512 tokens, batched) ...")
@@ -458,8 +477,8 @@ def main():
                 "kind": "port",
                 "sample": "the reference's sequential Q4 dequant-dot (main.rs:133-150) and "
                           "naive_matmul at m=1 on the dequantized weights "
-                          "(examples/bench/src/lib.rs:221-233), C restatement, 1 thread, "
-                          "repeated for 1 s each"}
+                          "(examples/bench/src/lib.rs:221-233), C restatement, 1 thread "
+                          "pinned to one core, repeated for 1 s each"}
     ctx.close()
     print(json.dumps(result), flush=True)
 

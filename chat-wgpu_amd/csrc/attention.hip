@@ -271,6 +271,10 @@ __global__ __launch_bounds__(64 * HPK) void attn_kernel(cwi::AttnArgs a, float s
 
     const int c = blockIdx.x, g = blockIdx.y;
     const int seq = a.pos_dev ? (*a.pos_dev + 1) : a.seq;
+    // a device-resident position past the cache (the host bounds the
+    // position it tracks; this covers a state it could not see): no KV
+    // row is written and nothing past the cache is read
+    if (seq < 1 || seq > a.max_seq) return;
     const int c0 = c * C::CP;
     if (c0 >= seq) return;
     const int n_chunks = (seq + C::CP - 1) / C::CP;
@@ -762,6 +766,10 @@ __global__ __launch_bounds__(64 * W) void attn_wave_kernel(cwi::AttnArgs a, floa
 
     const int c = blockIdx.x, g = blockIdx.y;
     const int seq = a.pos_dev ? (*a.pos_dev + 1) : a.seq;
+    // a device-resident position past the cache (the host bounds the
+    // position it tracks; this covers a state it could not see): no KV
+    // row is written and nothing past the cache is read
+    if (seq < 1 || seq > a.max_seq) return;
     const int c0 = c * C::CP;
     if (c0 >= seq) return;
     const int n_chunks = (seq + C::CP - 1) / C::CP;
@@ -1109,6 +1117,10 @@ __global__ __launch_bounds__(64 * MfmaCfg<HPK>::WMAX) void attn_mfma_kernel(cwi:
     const int CP = C::PW * W;
     const int c = blockIdx.x, g = blockIdx.y;
     const int seq = a.pos_dev ? (*a.pos_dev + 1) : a.seq;
+    // a device-resident position past the cache (the host bounds the
+    // position it tracks; this covers a state it could not see): no KV
+    // row is written and nothing past the cache is read
+    if (seq < 1 || seq > a.max_seq) return;
     const int c0 = c * CP;
     if (c0 >= seq) return;
     const int n_chunks = (seq + CP - 1) / CP;

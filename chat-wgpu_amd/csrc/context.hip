@@ -3,6 +3,7 @@
 // One stream per context; a deterministic per-frame arena; events for the
 // per-kernel profile.
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -109,14 +110,29 @@ static int refuse_while_capturing(const cw_ctx *ctx, const char *what) {
 int ctx_scratch(cw_ctx *ctx, size_t bytes, void **out) {
     if (bytes > ctx->scratch_size) {
         CW_TRY(refuse_while_capturing(ctx, "kernel scratch must grow"));
-        size_t sz = bytes < (1u << 20) ? (1u << 20) : bytes;
+        // geometric growth: a caller whose size creeps up (attention over a
+        // growing sequence) reallocates O(log n) times, not every few steps
+        size_t sz = std::max(bytes, std::max((size_t)1 << 20, 2 * ctx->scratch_size));
         void *p = nullptr;
         CW_HIP(hipMalloc(&p, sz));
-        // a launch sequence recorded earlier (cw_graph_*) still names the old
-        // buffer; replaying it must not write freed memory, so the old buffer
-        // is retired, not freed, until the context is destroyed
-        if (ctx->scratch) ctx->scratch_retired.push_back(ctx->scratch);
+        if (ctx->scratch) {
+            if (ctx->scratch_recorded) {
+                // a launch sequence recorded earlier (cw_graph_*) may name the
+                // old buffer; replaying it must not write freed memory, so it
+                // is retired, not freed, until the context is destroyed
+                ctx->scratch_retired.push_back(ctx->scratch);
+            } else {
+                // only queued launches use it: free it once they are done
+                hipError_t e = hipStreamSynchronize(ctx->stream);
+                if (e == hipSuccess) e = hipFree(ctx->scratch);
+                if (e != hipSuccess) {
+                    hipFree(p);
+                    return hip_fail(e, "ctx_scratch: releasing the old scratch", __FILE__, __LINE__);
+                }
+            }
+        }
         ctx->scratch = p;
+        ctx->scratch_recorded = false;
         // counters inside scratch must start at zero (cleared in stream order)
         CW_HIP(hipMemsetAsync(ctx->scratch, 0, sz, ctx->stream));
         ctx->scratch_size = sz;
@@ -415,6 +431,8 @@ int cw_graph_begin(cw_ctx *ctx) {
     }
     CW_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeRelaxed));
     ctx->capturing = true;
+    // the recording may name the current scratch: keep it alive when it grows
+    ctx->scratch_recorded = true;
     return CW_OK;
 }
 

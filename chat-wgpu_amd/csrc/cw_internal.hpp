@@ -101,11 +101,16 @@ struct cw_ctx {
     unsigned *attn_cnt = nullptr;
 
     // kernel scratch (attention partials, argmax partials, counters) for the
-    // standalone kernel entry points; grows on demand between launches
+    // standalone kernel entry points; grows on demand between launches, at
+    // least doubling each time
     void *scratch = nullptr;
     size_t scratch_size = 0;
-    // smaller scratch buffers a larger request replaced: a recorded launch
-    // sequence may still name them, so they live until cw_ctx_destroy
+    // a recording (cw_graph_begin) was opened while `scratch` was current, so
+    // a recorded launch sequence may name it
+    bool scratch_recorded = false;
+    // smaller scratch buffers a larger request replaced while a recording
+    // could name them: they live until cw_ctx_destroy (at most the sum of a
+    // doubling sequence, i.e. less than the current buffer)
     std::vector<void *> scratch_retired;
 
     // this device's static scratch of cw_attention_noalloc (set at create)
@@ -373,8 +378,14 @@ struct Extent {
 // counters), computed from the same phase table the kernel uses, must lie
 // inside one of `ext`.  `a.layers` must point at the host copy of the layer
 // table.  Returns false with the first offending range in *why.
-bool step_check_ranges(const StepArgs &a, int kv_dtype, int head_dim, int n_cu,
-                       const std::vector<Extent> &ext, std::string *why);
+// The check also covers the device argument block `args_dev` and layer
+// table `layers_dev` (sizeof(StepArgs), n_layers StepLayer), the dynamic and
+// static LDS of every phase, and the phase stamps when `a.trace` is set.
+bool step_check_ranges(const StepArgs &a, const void *args_dev, const void *layers_dev,
+                       int kv_dtype, int head_dim, int n_cu, const std::vector<Extent> &ext,
+                       std::string *why);
+// int64 phase stamps one launch writes when tracing
+size_t step_trace_words(int n_layers);
 
 size_t step_sync_words();
 int step_sync_err_index();

@@ -855,6 +855,28 @@ __device__ __forceinline__ const StepArgs *fresh(const StepArgs *p) {
 // The phases of one step, in order: per layer QKV, ATTN, O, GU, DOWN; then LM.
 enum { P_QKV = 0, P_ATTN = 1, P_O = 2, P_GU = 3, P_DOWN = 4, P_LM = 5 };
 
+// The kernel's static LDS (one struct, so the host check sizes it exactly).
+struct StepShared {
+    float red[kW];                       // RMSNorm partial sums per wave
+    int ok_s;                            // grid barrier completed
+    int merge_s[1 + cwi::kStepMaxKv];    // kv heads this workgroup merges
+    float best_v[kW];                    // argmax per wave
+    uint32_t best_i[kW];
+    int last_s;                          // last workgroup of the argmax merge
+};
+
+// The end (bytes) of the dynamic LDS a GEMV phase of input width K touches:
+// x as [8][K/32] float4 from offset 0, the block sums from the fixed offset
+// 8 * (kMaxK / 32) float4.
+__host__ __device__ inline size_t gemv_lds_end(int K) {
+    return (size_t)8 * (kMaxK / 32) * 16 + (size_t)(K / 32) * 4;
+}
+// ... and of an attention phase: IPW item tiles of ILDS bytes each.
+template <typename KVT, int HPK>
+__host__ __device__ inline size_t attn_lds_end() {
+    return (size_t)At<KVT, HPK>::IPW * At<KVT, HPK>::ILDS;
+}
+
 // What a GEMV phase reads and writes, from (layer, kind).
 struct PhaseSpec {
     const uint8_t *q;
@@ -934,6 +956,9 @@ __host__ __device__ inline PhaseSpec phase_spec(const StepArgs &a, int l, int ki
 
 // ---------------------------------------------------------------- host-side range check
 
+template <typename KVT>
+int attn_lds_of(int hpk);
+
 struct RangeCheck {
     const std::vector<cwi::Extent> &ext;
     std::string *why;
@@ -975,9 +1000,37 @@ const char *kPhaseName[6] = {"QKV", "ATTN", "O", "GATE|UP", "DOWN", "LM head"};
 
 namespace cwi {
 
-bool step_check_ranges(const StepArgs &a, int kv_dtype, int head_dim, int n_cu,
-                       const std::vector<Extent> &ext, std::string *why) {
+bool step_check_ranges(const StepArgs &a, const void *args_dev, const void *layers_dev,
+                       int kv_dtype, int head_dim, int n_cu, const std::vector<Extent> &ext,
+                       std::string *why) {
     RangeCheck rc{ext, why};
+    // the argument block every phase re-reads (`fresh`) and the layer table
+    rc.need(args_dev, sizeof(StepArgs), "step argument block", 0);
+    rc.need(layers_dev, (size_t)a.n_layers * sizeof(StepLayer), "layer table", 0);
+    // LDS: the dynamic size the launch passes must cover every phase's
+    // extent, and with the static block fit the CU's 160 KiB
+    const int hpk = a.n_heads / a.n_kv;
+    const size_t dyn = (size_t)step_lds_bytes(kv_dtype, hpk, a.max_seq);
+    const size_t at_end = kv_dtype == CW_F16 ? attn_lds_of<_Float16>(hpk) : attn_lds_of<float>(hpk);
+    const int q_dim_i = a.n_heads * head_dim;
+    for (int K : {a.dim, q_dim_i, a.hidden}) {
+        if (rc.ok && gemv_lds_end(K) > dyn) {
+            rc.ok = false;
+            *why = "a GEMV phase of input width " + std::to_string(K) + " touches " +
+                   std::to_string(gemv_lds_end(K)) + " bytes of LDS, the launch passes " +
+                   std::to_string(dyn);
+        }
+    }
+    if (rc.ok && at_end > dyn) {
+        rc.ok = false;
+        *why = "the attention phase touches " + std::to_string(at_end) +
+               " bytes of LDS, the launch passes " + std::to_string(dyn);
+    }
+    if (rc.ok && dyn + sizeof(StepShared) > (size_t)160 * 1024) {
+        rc.ok = false;
+        *why = "dynamic + static LDS (" + std::to_string(dyn + sizeof(StepShared)) +
+               " bytes) exceed 160 KiB";
+    }
     const size_t es = kv_dtype == CW_F16 ? 2 : 4;
     const size_t q_dim = (size_t)a.n_heads * head_dim, kv_dim = (size_t)a.n_kv * head_dim;
     const size_t qkv_n = q_dim + 2 * kv_dim;
@@ -1036,7 +1089,8 @@ bool step_check_ranges(const StepArgs &a, int kv_dtype, int head_dim, int n_cu,
         rc.ok = false;
         *why = "attention partials hold fewer chunks than the cache can need";
     }
-    // the argmax merge, the counters and the decode state
+    // the argmax merge (one slot per workgroup: the grid is one workgroup
+    // per CU), the counters and the decode state
     rc.need(a.am_v, (size_t)n_cu * 4, "LM head argmax values", a.n_layers);
     rc.need(a.am_i, (size_t)n_cu * 4, "LM head argmax ids", a.n_layers);
     rc.need(a.sync, step_sync_words() * 4, "grid counters", a.n_layers);
@@ -1045,8 +1099,14 @@ bool step_check_ranges(const StepArgs &a, int kv_dtype, int head_dim, int n_cu,
     rc.need(a.prompt, (size_t)a.max_seq * 4, "prompt ids", a.n_layers);
     rc.need(a.tokens, (size_t)a.max_seq * 4, "produced ids", a.n_layers);
     rc.need(a.argmax_out, 4, "argmax output", a.n_layers);
+    // the phase stamps, when on: [2e], [2e + 1] per barrier e <= 5L, the
+    // end at [10L + 2], two per phase from [10L + 4]
+    if (a.trace)
+        rc.need(a.trace, step_trace_words(a.n_layers) * 8, "phase stamps", a.n_layers);
     return rc.ok;
 }
+
+size_t step_trace_words(int n_layers) { return (size_t)20 * n_layers + 8; }
 
 }  // namespace cwi
 
@@ -1057,12 +1117,13 @@ namespace {
 template <typename KVT, int HPK>
 __global__ __launch_bounds__(kT) void decode_step_kernel(const StepArgs *__restrict__ ap) {
     extern __shared__ float4 lds4[];
-    __shared__ float red[kW];
-    __shared__ int ok_s;
-    __shared__ int merge_s[1 + cwi::kStepMaxKv];
-    __shared__ float best_v[kW];
-    __shared__ uint32_t best_i[kW];
-    __shared__ int last_s;
+    __shared__ StepShared sh;
+    float *red = sh.red;
+    int &ok_s = sh.ok_s;
+    int *merge_s = sh.merge_s;
+    float *best_v = sh.best_v;
+    uint32_t *best_i = sh.best_i;
+    int &last_s = sh.last_s;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int gw = blockIdx.x * kW + wave, nw = gridDim.x * kW;

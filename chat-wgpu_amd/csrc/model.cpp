@@ -302,6 +302,7 @@ int ensure_graph(cw_model *m) {
     const bool prof = ctx->profiling;
     ctx->profiling = false;
     CW_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeRelaxed));
+    ctx->scratch_recorded = true;  // (the step uses the model's own buffers)
     int rc = enqueue_step(m);
     hipGraph_t graph = nullptr;
     hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
@@ -351,19 +352,28 @@ int run_steps(cw_model *m, int n, int mode) {
             return CW_ERR_ARG;
         }
         const auto &c = m->cfg;
-        for (int i = 0; i < n; ++i)
+        for (int i = 0; i < n; ++i) {
             CW_TRY(launch_decode_step(m->ctx, m->step_dev, c.kv_dtype, c.n_heads / c.n_kv_heads,
                                       c.max_seq));
+            ++m->host_pos;
+        }
     } else if (mode == CW_STEP_GRAPH) {
         CW_TRY(ensure_graph(m));
-        for (int i = 0; i < n; ++i) CW_HIP(hipGraphLaunch(m->graph_exec, m->ctx->stream));
+        for (int i = 0; i < n; ++i) {
+            CW_HIP(hipGraphLaunch(m->graph_exec, m->ctx->stream));
+            ++m->host_pos;
+        }
     } else if (mode == CW_STEP_EAGER) {
-        for (int i = 0; i < n; ++i) CW_TRY(enqueue_step(m));
+        // a step advances the device position in its last launch (the LM
+        // head's epilogue): a step whose launches failed part-way never does
+        for (int i = 0; i < n; ++i) {
+            CW_TRY(enqueue_step(m));
+            ++m->host_pos;
+        }
     } else {
         set_error("unknown step mode %d", mode);
         return CW_ERR_ARG;
     }
-    m->host_pos += n;
     return CW_OK;
 }
 
@@ -444,7 +454,8 @@ bool check_step(cw_model *m, const std::vector<StepLayer> &host) {
     a.layers = host.data();
     std::string why;
     const int n_cu = m->dry ? m->dry_n_cu : m->ctx->n_cu;
-    if (step_check_ranges(a, m->cfg.kv_dtype, m->cfg.head_dim, n_cu, m->extents, &why))
+    if (step_check_ranges(a, m->step_dev, m->step_layers, m->cfg.kv_dtype, m->cfg.head_dim, n_cu,
+                          m->extents, &why))
         return true;
     snprintf(m->fused_why, sizeof m->fused_why, "buffer layout check failed: %s", why.c_str());
     return false;
@@ -1180,7 +1191,7 @@ int cw_model_profile_step(cw_model *m, int64_t *ticks, int max_n, int *n_out, do
     CW_HIP(hipMemcpyAsync(&s, m->state, sizeof s, hipMemcpyDeviceToHost, m->ctx->stream));
     CW_HIP(hipStreamSynchronize(m->ctx->stream));
     CW_CHECK_ARG(s.pos < m->cfg.max_seq, "cw_model_profile_step: pos %d at max_seq", s.pos);
-    const int n = 20 * m->cfg.n_layers + 8;  // stamps written by one launch
+    const int n = (int)step_trace_words(m->cfg.n_layers);  // stamps written by one launch
     long long *dev = nullptr;
     StepArgs *args_dev = nullptr;
     CW_HIP(hipMalloc(&dev, (size_t)n * 8 + sizeof(StepArgs)));

@@ -165,6 +165,26 @@ def test_rope(ctx, rng):
         assert np.max(np.abs(y - ref)) <= 2e-6 * np.max(np.abs(ref))
 
 
+def test_rope_rotation_direction_one_hot(ctx):
+    """The device rotation's sign (rope.wgsl:30-31): a one-hot input at i gives
+    (cos, sin) in (y_i, y_{i+h}), one at i + h gives (-sin, cos), against
+    numpy's f64 cos/sin of pos * theta^(-2i/hd); every other element stays 0."""
+    hd, theta, h = 128, 1e6, 64
+    probes = [(i, j) for i in (0, 1, 5, 31, h - 1) for j in (i, i + h)]
+    x = np.zeros((len(probes), hd), np.float32)
+    for r, (_, j) in enumerate(probes):
+        x[r, j] = 1.0
+    for pos in (1, 7, 100, 4351):
+        y = ctx.rope(ctx.storage(x.ravel()), len(probes), hd, pos, theta).download()
+        y = y.reshape(len(probes), hd)
+        for r, (i, j) in enumerate(probes):
+            f = pos * float(np.float32(theta)) ** (-2.0 * i / hd)
+            c, s = np.cos(f), np.sin(f)
+            want = np.zeros(hd)
+            want[i], want[i + h] = (c, s) if j == i else (-s, c)
+            assert np.max(np.abs(y[r] - want)) < 2e-7, (pos, i, j)
+
+
 def test_add_swiglu_kats(ctx):
     k = KATS["swiglu_const"]
     n = k["n"]

@@ -254,6 +254,86 @@ def test_qwen3_8b_teacher_forced_over_the_decode_range(ctx):
     o.close()
 
 
+# ---------------------------------------------------------------- a greedy horizon that moves
+
+HORIZON = 64
+
+
+@pytest.fixture(scope="module")
+def horizon(ctx):
+    """Qwen3-8B shape from a cache of 4096 positions of N(0,1) f16, 64 greedy
+    steps replayed as a HIP graph, with two changes to the benchmark model so
+    that each produced id depends on the fed one: embedding rows drawn with
+    std 1e5, and an untied output head (output.weight, which Qwen3::load
+    uses when present, qwen3.rs:93-98) drawn like the layer projections.
+
+    With the benchmark model itself every step returns one id: the Q4
+    weights' (q - 8) has mean -1/2, so the final hidden state lies along one
+    fixed direction whatever the token, and the tied head's argmax is the
+    embedding row with the extreme sum there (embedding std 0.02 and 1.0
+    both give that id at every step, top-2 margin 0.03 and 1.9).  A loop
+    that fed back a stale token would pass such a test; here it cannot."""
+    pre, seed = 4096, 8008
+    cfg = qwen3_8b(pre + HORIZON)
+    w = cw.synthetic_weights(cfg, seed)
+    w["token_embd.weight"] = cw.synth_normal_f32(cw.synth_key(seed, "token_embd.weight"),
+                                                 cfg.vocab * cfg.dim, 0.0, 1e5)
+    w["output.weight"] = cw.synth_q4(cw.synth_key(seed, "output.weight"), cfg.vocab, cfg.dim)
+    kv_n = cfg.n_layers * pre * cfg.n_kv_heads * cfg.head_dim
+    k = cw.synth_normal_f16(cw.synth_key(seed, "kv.k"), kv_n)
+    v = cw.synth_normal_f16(cw.synth_key(seed, "kv.v"), kv_n)
+    start = cw.synth_tokens(cw.synth_key(seed, "start"), 1, cfg.vocab)
+    m, o = build_pair(ctx, cfg, w)
+    m.prefill_kv(k, v, pre)
+    o.prefill_kv(k, v, pre)
+    del k, v, w
+    orc.set_threads(16)
+    print(f"\n[qwen3-8b horizon] {HORIZON} greedy steps from {pre} on the GPU", flush=True)
+    toks = m.generate(start, HORIZON, start_pos=pre, mode=cw.STEP_GRAPH)
+    state = {"m": m, "o": o, "pre": pre, "start": start, "gpu": toks, "ref": []}
+    yield state
+    m.close()
+    o.close()
+
+
+def horizon_half(h, first):
+    """The oracle's greedy ids for one half of the horizon (the second half
+    resumes the oracle's own trajectory), compared with the GPU's."""
+    n = HORIZON // 2
+    if first:
+        ref, margins = h["o"].generate(h["start"], n, start_pos=h["pre"])
+    else:
+        assert len(h["ref"]) == n, "the first half did not pass"
+        last = np.array([h["ref"][-1]], np.uint32)
+        ref, margins = h["o"].generate(last, n, start_pos=h["pre"] + n)
+    lo = 0 if first else n
+    gpu = h["gpu"][lo:lo + n]
+    print(f"\n[qwen3-8b horizon] steps {lo}..{lo + n - 1}: ids {ref.tolist()}\n"
+          f"  top-2 margins min {float(np.min(margins)):.3e} "
+          f"{np.round(margins, 3).tolist()}", flush=True)
+    first_diff = np.nonzero(gpu != ref)[0]
+    msg = "" if not first_diff.size else (
+        f"first divergence at step {lo + first_diff[0]}: gpu {gpu[first_diff[0]]} oracle "
+        f"{ref[first_diff[0]]}, oracle top-2 margin {margins[first_diff[0]]:.3e}")
+    assert np.array_equal(gpu, ref), msg
+    h["ref"] += ref.tolist()
+
+
+def test_qwen3_8b_greedy_horizon_first_half(horizon):
+    horizon_half(horizon, True)
+
+
+def test_qwen3_8b_greedy_horizon_second_half(horizon):
+    horizon_half(horizon, False)
+    ids = horizon["ref"]
+    distinct = len(set(ids))
+    print(f"\n[qwen3-8b horizon] {distinct} distinct ids over {len(ids)} steps", flush=True)
+    assert len(ids) == HORIZON and distinct >= 4, distinct
+    # every produced id is fed back: a loop that kept feeding one token would
+    # repeat one id, which the trajectory above does not
+    assert any(ids[i] != ids[i + 1] for i in range(len(ids) - 1))
+
+
 # ---------------------------------------------------------------- fused decode step
 
 # The persistent decode-step kernel raised an illegal memory access here

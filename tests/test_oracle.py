@@ -257,6 +257,50 @@ def test_rope_table_vs_numpy_and_f32_literal(rng):
         assert np.max(np.abs(a - b)) < 1e-4 * max(1, pos)
 
 
+def rope_one_hot_mismatch(rot, hd=128, theta=1e6, positions=(1, 7, 100, 4351)):
+    """The rotation direction fixed by rope.wgsl:30-31 (y_i = x_i c - x_{i+h} s,
+    y_{i+h} = x_{i+h} c + x_i s): a one-hot input at i must give (c, s) in
+    (y_i, y_{i+h}), one at i + h must give (-s, c), with c, s = cos, sin of
+    pos * theta^(-2i/hd) from numpy in f64.  `rot(x, pos)` is the rotation
+    under test; returns the largest deviation over the probes (pair indices
+    spread over the head, including the fastest and slowest frequencies)."""
+    h = hd // 2
+    worst = 0.0
+    for pos in positions:
+        for i in (0, 1, 5, 31, h - 1):
+            f = pos * float(np.float32(theta)) ** (-2.0 * i / hd)
+            c, s = np.cos(f), np.sin(f)
+            e = np.zeros(hd, np.float32)
+            e[i] = 1.0
+            y = rot(e, pos)
+            worst = max(worst, abs(y[i] - c), abs(y[i + h] - s))
+            others = np.delete(y, [i, i + h])
+            worst = max(worst, float(np.max(np.abs(others))))
+            e = np.zeros(hd, np.float32)
+            e[i + h] = 1.0
+            y = rot(e, pos)
+            worst = max(worst, abs(y[i] + s), abs(y[i + h] - c))
+    return worst
+
+
+def test_rope_rotation_direction_one_hot():
+    """Pins the sign of the rotation, which the identity at pos 0, the norm
+    preservation and the relative-position invariance leave open: both
+    oracle forms against numpy's cos/sin in the signs of rope.wgsl:30-31,
+    and the check itself fails for the opposite rotation."""
+    hd, theta = 128, 1e6
+    assert rope_one_hot_mismatch(lambda x, p: orc.rope(x, 1, hd, p, theta)) < 2e-7
+    # the literal f32 form drifts by ~pos * ulp(freq) (see the table test)
+    assert rope_one_hot_mismatch(lambda x, p: orc.rope_f32_literal(x, 1, hd, p, theta),
+                                 positions=(1, 7, 100)) < 1e-4
+
+    def flipped(x, p):  # rotation by -angle: M R M with M = diag(1, -1) per pair
+        h = hd // 2
+        y = orc.rope(np.concatenate([x[:h], -x[h:]]), 1, hd, p, theta)
+        return np.concatenate([y[:h], -y[h:]])
+    assert rope_one_hot_mismatch(flipped) > 0.1
+
+
 def test_attention_kats_and_truth(rng):
     k = KATS["attention_seq1"]
     nh, nkv, hd = k["n_heads"], k["n_kv"], k["head_dim"]

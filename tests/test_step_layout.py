@@ -7,7 +7,10 @@ allocation.  With gate and up as two allocations (split_gate_up) while the
 step reads them as one [2*hidden][dim] matrix, the gate|up phase of layer 0
 runs `hidden` rows past the gate matrix: the check must name that range.
 The model's own layout (gate|up in one allocation) must pass for every
-shape the GPU tests run the fused step on."""
+shape the GPU tests run the fused step on.  The check also covers the
+device argument block and layer table the kernel reads, the dynamic and
+static LDS every phase touches, the per-workgroup argmax slots of a grid of
+one workgroup per CU, the grid counters and, when tracing, the stamps."""
 import pytest
 
 import cw
@@ -20,6 +23,8 @@ def small128(max_seq, kv_dtype=cw.CW_F32, n_heads=4, n_kv=2):
 
 
 CONFIGS = [
+    # the configuration whose one GPU run after the gate|up fix faulted
+    cw.make_config(2, 256, 4, 2, 128, 512, 1000, 8),
     small128(29, cw.CW_F32, 4, 2),
     small128(29, cw.CW_F16, 8, 2),
     small128(29, cw.CW_F32, 2, 2),
