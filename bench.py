@@ -32,6 +32,7 @@ import cw  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 PRE = 4096
+DECODE = 256  # the 8B workload: 256 greedy steps from a 4096-position cache
 
 
 def log(msg):
@@ -308,6 +309,10 @@ def main():
                     help="for rocprofv3 --pmc runs: one 256 MiB device-to-device copy (the "
                          "counter calibration), then 4 eager decode steps of the workload; "
                          "prints no JSON")
+    ap.add_argument("--graph-probe", type=int, default=0, metavar="N",
+                    help="for rocprofv3 kernel traces of the replayed step: 8 + N decode steps "
+                         "of the workload, each one graph launch followed by the next (the chat "
+                         "loop's pattern); prints no JSON")
     ap.add_argument("--prefill-only", action="store_true",
                     help="for rocprofv3 traces of the batched prefill: build the 8B model and "
                          "print only the 512-token prefill figures (one JSON line)")
@@ -321,8 +326,8 @@ def main():
     ctx = cw.Context(0)
     info = ctx.info()
     log(f"device {info}")
-    cfg = cw.make_config(36, 4096, 32, 8, 128, 12288, 151936, PRE + max(K, W, 8) + 1, cw.CW_F16,
-                         1e-6, 1e6)
+    cfg = cw.make_config(36, 4096, 32, 8, 128, 12288, 151936, PRE + max(DECODE, K, W, 8) + 1,
+                         cw.CW_F16, 1e-6, 1e6)
     t = time.perf_counter()
     weights = cw.synthetic_weights(cfg, 8008)
     log(f"synthetic weights generated in {time.perf_counter() - t:.1f}s")
@@ -355,13 +360,30 @@ def main():
         ctx.close()
         return
 
+    if args.graph_probe:
+        m.reset_state(start, PRE)
+        for _ in range(8 + args.graph_probe):
+            m.decode_async(1, mode=cw.STEP_GRAPH)
+        ctx.flush()
+        log("graph probe done")
+        m.close()
+        ctx.close()
+        return
+
     m.reset_state(start, PRE)
     m.decode_async(W, mode=cw.STEP_GRAPH)
     ctx.flush()
     log("warmup done")
 
-    # timed: K decode steps from position PRE, the step replayed as a HIP graph
+    # timed: K decode steps of the 256-step workload, the step replayed as a
+    # HIP graph.  Fewer than 256 timed steps sit at the middle of the
+    # workload (the steps before them run untimed first), so the timed
+    # window's mean cache length is the workload's own.
+    skip = max(0, (DECODE - K) // 2)
+    t0pos = PRE + skip
     m.reset_state(start, PRE)
+    if skip:
+        m.decode_async(skip, mode=cw.STEP_GRAPH)
     ctx.flush()
     t0 = time.perf_counter()
     m.decode_async(K, mode=cw.STEP_GRAPH)
@@ -389,7 +411,7 @@ def main():
     log("per-token kernel ms (eager, kernel timestamps): " +
         ", ".join(f"{n}={ms:.3f}" for n, (_, ms) in prof.items()))
     traffic, traffic_src = committed_gemv_traffic()
-    bytes_avg = sum(step_bytes(cfg, PRE + i + 1, 2)[0] for i in range(K)) / K
+    bytes_avg = sum(step_bytes(cfg, t0pos + i + 1, 2)[0] for i in range(K)) / K
 
     result = {
         "metric": "decode tokens/s (Qwen3-0.6B/8B Q4_0, 1 GPU); Q4 GEMV HBM GB/s vs peak",
@@ -404,8 +426,9 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded Q4_0 weights, N(0,1) f16 KV pre-fill)",
-        "config": {"workload": "qwen3-8b-shape q4_0 greedy decode, batch 1, KV 4096->"
-                               f"{PRE + K} f16, {K} steps, step replayed as a HIP graph",
+        "config": {"workload": f"qwen3-8b-shape q4_0 greedy decode, batch 1, f16 KV prefilled "
+                               f"to {PRE}, {DECODE}-step decode; timed steps {skip}..{skip + K - 1} "
+                               f"(KV {t0pos + 1}->{t0pos + K}), step replayed as a HIP graph",
                    "weights": "q4_0", "hidden": 4096, "layers": 36, "heads": "32/8x128",
                    "intermediate": 12288, "vocab": 151936, "kv_prefill": PRE,
                    "parallelism": "single GPU"},

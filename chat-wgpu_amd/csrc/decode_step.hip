@@ -39,6 +39,15 @@
 
 #include "cw_internal.hpp"
 
+// Hooks for a CPU execution of the kernel (tests/step_emu): compiler barriers
+// that pin a value in a scalar / vector register, and the workgroup's LDS.
+#ifndef CW_STEP_HOOKS
+#define CW_OPAQUE_S(v) asm volatile("" : "+s"(v))
+#define CW_OPAQUE_V(v) asm volatile("" : "+v"(v))
+#define CW_WG_SHARED(T, name) __shared__ T name
+#define CW_WG_DYNAMIC(T, name) extern __shared__ T name[]
+#endif
+
 namespace {
 
 using cwi::StepArgs;
@@ -107,13 +116,13 @@ __device__ __forceinline__ void drain() {
 // the phase rather than hoisted out of the layer loop and kept live across it.
 __device__ __forceinline__ int opaque(int v) {
     v = __builtin_amdgcn_readfirstlane(v);
-    asm volatile("" : "+s"(v));
+    CW_OPAQUE_S(v);
     return v;
 }
 // the thread index, re-read per phase for the same reason
 __device__ __forceinline__ int tid_() {
     int v = (int)threadIdx.x;
-    asm volatile("" : "+v"(v));
+    CW_OPAQUE_V(v);
     return v;
 }
 
@@ -848,7 +857,8 @@ __device__ __forceinline__ const StepArgs *fresh(const StepArgs *p) {
     const uint64_t v = reinterpret_cast<uint64_t>(p);
     uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
     uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    asm volatile("" : "+s"(lo), "+s"(hi));
+    CW_OPAQUE_S(lo);
+    CW_OPAQUE_S(hi);
     return reinterpret_cast<const StepArgs *>(((uint64_t)hi << 32) | lo);
 }
 
@@ -1116,8 +1126,8 @@ namespace {
 // the code: the loop body stays small enough for the instruction cache.
 template <typename KVT, int HPK>
 __global__ __launch_bounds__(kT) void decode_step_kernel(const StepArgs *__restrict__ ap) {
-    extern __shared__ float4 lds4[];
-    __shared__ StepShared sh;
+    CW_WG_DYNAMIC(float4, lds4);
+    CW_WG_SHARED(StepShared, sh);
     float *red = sh.red;
     int &ok_s = sh.ok_s;
     int *merge_s = sh.merge_s;

@@ -774,6 +774,43 @@ int cw_step_layout_check(const cw_model_config *cfg, int n_cu, int split_gate_up
     return CW_OK;
 }
 
+int cw_step_dry_plan(const cw_model_config *cfg, int n_cu, int split_gate_up, void *args_out,
+                     size_t args_len, void *layers_out, size_t layers_len, void **ext_ptr,
+                     size_t *ext_bytes, int max_ext, int *n_ext) {
+    CW_CHECK_ARG(cfg && n_cu > 0 && args_out && layers_out && ext_ptr && ext_bytes && n_ext,
+                 "cw_step_dry_plan: bad argument");
+    CW_TRY(check_config(*cfg, "cw_step_dry_plan"));
+    cw_model m;
+    m.dry = true;
+    m.dry_split_gu = split_gate_up != 0;
+    m.dry_n_cu = n_cu;
+    m.dry_next = (uintptr_t)1 << 44;
+    CW_TRY(model_alloc(&m, *cfg));
+    m.fused_unsupported = step_unsupported(cfg->head_dim, cfg->n_heads / cfg->n_kv_heads,
+                                           cfg->n_kv_heads, cfg->dim, m.q_dim, cfg->hidden,
+                                           cfg->max_seq);
+    CW_CHECK_ARG(m.fused_unsupported == nullptr,
+                 "cw_step_dry_plan: the fused step does not cover this config: %s",
+                 m.fused_unsupported);
+    std::vector<StepLayer> host;
+    CW_TRY(build_step(&m, host));
+    CW_CHECK_ARG(args_len >= sizeof(StepArgs), "cw_step_dry_plan: args_len %zu < %zu", args_len,
+                 sizeof(StepArgs));
+    CW_CHECK_ARG(layers_len >= host.size() * sizeof(StepLayer),
+                 "cw_step_dry_plan: layers_len %zu < %zu", layers_len,
+                 host.size() * sizeof(StepLayer));
+    CW_CHECK_ARG((int)m.extents.size() <= max_ext, "cw_step_dry_plan: %zu allocations > %d",
+                 m.extents.size(), max_ext);
+    memcpy(args_out, &m.step, sizeof(StepArgs));
+    memcpy(layers_out, host.data(), host.size() * sizeof(StepLayer));
+    for (size_t i = 0; i < m.extents.size(); ++i) {
+        ext_ptr[i] = const_cast<void *>(m.extents[i].p);
+        ext_bytes[i] = m.extents[i].bytes;
+    }
+    *n_ext = (int)m.extents.size();
+    return CW_OK;
+}
+
 int cw_model_destroy(cw_model *m) {
     if (!m) return CW_OK;
     CW_TRY(refuse_recording(m, "cw_model_destroy"));

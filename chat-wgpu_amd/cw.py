@@ -116,6 +116,8 @@ _SIGS = {
     "cw_model_tokens": (_I, [_P, _P, _I, C.POINTER(_I)]),
     "cw_model_profile_step": (_I, [_P, _P, _I, C.POINTER(_I), C.POINTER(C.c_double)]),
     "cw_step_layout_check": (_I, [C.POINTER(ModelConfig), _I, _I, C.c_char_p, _SZ]),
+    "cw_step_dry_plan": (_I, [C.POINTER(ModelConfig), _I, _I, _P, _SZ, _P, _SZ, _P, _P, _I,
+                              C.POINTER(_I)]),
     "cw_gguf_open": (_I, [C.c_char_p, C.POINTER(_P)]),
     "cw_gguf_parse": (_I, [_P, _SZ, C.POINTER(_P)]),
     "cw_gguf_close": (_I, [_P]),

@@ -301,6 +301,18 @@ int cw_model_profile_step(cw_model *m, int64_t *ticks, int max_n, int *n_out, do
  * CW_ERR_ARG for configs the fused step does not cover. */
 int cw_step_layout_check(const cw_model_config *cfg, int n_cu, int split_gate_up, char *why,
                          size_t why_len);
+/* No counterpart in the reference: for a CPU execution of the CW_STEP_FUSED
+ * kernel (tests/step_emu).  The same unmapped buffer plan as
+ * cw_step_layout_check, without its range check: copies the step's argument
+ * block (args_len bytes of the library's internal StepArgs) and its layer
+ * table (layers_len bytes, n_layers internal StepLayer records) and lists
+ * every planned allocation as (ext_ptr[i], ext_bytes[i]), i < *n_ext <=
+ * max_ext, so a caller can back each one with real memory of exactly that
+ * size and relocate the pointers.  CW_ERR_ARG when a length is too small or
+ * the fused step does not cover cfg. */
+int cw_step_dry_plan(const cw_model_config *cfg, int n_cu, int split_gate_up, void *args_out,
+                     size_t args_len, void *layers_out, size_t layers_len, void **ext_ptr,
+                     size_t *ext_bytes, int max_ext, int *n_ext);
 /* The prompt phase of model::generate (src/model/mod.rs:57-125: P forwards,
  * the logits of all but the last discarded) for n tokens at positions
  * start_pos..start_pos+n-1, batched: each layer runs as Q4_0 GEMMs on the
