@@ -282,6 +282,9 @@ ATTN_CASES = [  # (n_heads, n_kv, hd, seq, f16)
     (8, 8, 128, 777, True), (16, 2, 128, 513, True),
     # the f32 head_dim-128 kernel at the same groupings
     (8, 8, 128, 300, False), (8, 1, 128, 200, False),
+    # the longest sequence an attention call takes (32768 positions), on
+    # the 8B shape's heads
+    (32, 8, 128, 32768, True), (32, 8, 128, 32768, False),
 ]
 
 
@@ -295,6 +298,15 @@ def test_attention_vs_oracle(ctx, rng, nh, nkv, hd, seq, f16):
     ref = orc.attention(q, k, v, f16, nh, nkv, seq, hd)
     vmax = np.max(np.abs(v.view(np.float16) if f16 else v))
     assert np.max(np.abs(o - ref)) <= 1e-5 * vmax
+
+
+def test_attention_refuses_sequences_past_its_limit(ctx):
+    buf = ctx.empty(16)
+    for seq in (0, 32769):
+        rc = cw.lib().cw_attention(ctx.h, buf.ptr, buf.ptr, buf.ptr, cw.CW_F16, 32, 8, seq, 128,
+                                   buf.ptr)
+        assert rc == cw.CW_ERR_ARG, seq
+        assert "seq=" in cw.lib().cw_last_error().decode()
 
 
 def test_attention_repeated_calls(ctx, rng):
