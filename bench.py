@@ -230,6 +230,42 @@ def bench_single_gemv(ctx, out_f=3072, in_f=1024, pool_bytes=600 << 20, passes=3
     return ms * 1e3 / cnt, q4_bytes(out_f, in_f) + 4 * in_f + 4 * out_f, n
 
 
+def small_probe(ctx, passes=3):
+    """The small configurations' kernels, for a kernel trace: the 0.6B-shape
+    model's 32-token prompt and 8 greedy steps (graph-replayed), 8 eager
+    decode steps from the end of the prompt, then `passes` passes of the
+    3072x1024 GEMV over the rotating pool of bench_single_gemv (no library
+    profiling, so the trace's own timestamps are the only ones taken)."""
+    P = 32
+    cfg = cw.make_config(28, 1024, 16, 8, 128, 3072, 151936, P + 128, cw.CW_F32, 1e-6, 1e6)
+    m = cw.Model(ctx, cfg)
+    m.load_synthetic(2024)
+    m.finalize()
+    prompt = cw.synth_tokens(cw.synth_key(2024, "prompt"), P, cfg.vocab)
+    m.generate(prompt, 8, mode=cw.STEP_GRAPH)
+    m.reset_state(int(prompt[-1]), P)
+    m.decode_async(8, mode=cw.STEP_EAGER)
+    ctx.flush()
+    m.close()
+    log("0.6B steps done")
+    out_f, in_f = 3072, 1024
+    s, q = cw.synth_q4(cw.synth_key(7, "c0.w"), out_f, in_f)
+    x = cw.synth_normal_f32(cw.synth_key(7, "c0.x"), in_f)
+    n = max(2, (600 << 20) // (s.nbytes + q.nbytes))
+    pool = [(ctx.storage(s), ctx.storage(q)) for _ in range(n)]
+    xd, yd = ctx.storage(x), ctx.empty(out_f, np.float32)
+    for _ in range(1 + passes):  # the first pass warms
+        for sd, qd in pool:
+            ctx.q4_gemv(xd, sd, qd, in_f, out_f, y=yd)
+    ctx.flush()
+    log(f"3072x1024 GEMV: {1 + passes} passes over {n} weight copies done")
+    for sd, qd in pool:
+        ctx.free(sd)
+        ctx.free(qd)
+    ctx.free(xd)
+    ctx.free(yd)
+
+
 def bench_read_probe(ctx, nbytes=2 << 30, passes=4):
     """Achievable HBM read bandwidth: the read probe (cw_hbm_read_probe, the
     examples/q4probe.rs analogue) streams one 2 GiB buffer (8x the 256 MB
@@ -313,6 +349,11 @@ def main():
                     help="for rocprofv3 kernel traces of the replayed step: 8 + N decode steps "
                          "of the workload, each one graph launch followed by the next (the chat "
                          "loop's pattern); prints no JSON")
+    ap.add_argument("--small-probe", action="store_true",
+                    help="for rocprofv3 kernel traces of the small configurations: 8 eager decode "
+                         "steps of the Qwen3-0.6B-shape model after its 32-token prompt, then "
+                         "3 passes of the 3072x1024 GEMV over its rotating weight pool; prints "
+                         "no JSON")
     ap.add_argument("--prefill-only", action="store_true",
                     help="for rocprofv3 traces of the batched prefill: build the 8B model and "
                          "print only the 512-token prefill figures (one JSON line)")
@@ -326,6 +367,10 @@ def main():
     ctx = cw.Context(0)
     info = ctx.info()
     log(f"device {info}")
+    if args.small_probe:
+        small_probe(ctx)
+        ctx.close()
+        return
     cfg = cw.make_config(36, 4096, 32, 8, 128, 12288, 151936, PRE + max(DECODE, K, W, 8) + 1,
                          cw.CW_F16, 1e-6, 1e6)
     t = time.perf_counter()

@@ -790,7 +790,10 @@ __global__ __launch_bounds__(64 * W) void attn_wave_kernel(cwi::AttnArgs a, floa
     // used: a query head (head g*HPK + wave, clamped; only waves below HPK
     // use it), the new k and v and their RoPE row (used by the wave holding
     // pos_new), then this wave's K rows and V rows (rows past the sequence
-    // clamped to its last row and masked later) ----
+    // clamped to its last row and masked later).  Issuing the rows before
+    // the position is read, as the f16 kernel does, measured slower here
+    // (Qwen3-0.6B-shape token loop, f32 cache of 160 positions: 1405-1419
+    // against 1425-1437 tokens/s) ----
     const int h = g * HPK + (wave < HPK ? wave : HPK - 1);
     const bool q_wave = wave < HPK;
     // a wave that does not use a vector still issues its load, over a buffer
@@ -956,7 +959,14 @@ __global__ __launch_bounds__(64 * W) void attn_wave_kernel(cwi::AttnArgs a, floa
             l[hh] = ls;
         }
 
-        // ---- 6. P.V over the lane's rows, summed over the row groups ----
+        // ---- 6. P.V over the lane's rows, summed over the row groups.  Rows
+        // at or past the sequence were clamped to its last row, pos_new when
+        // fused, whose loaded value is the cache's old one (this launch
+        // writes the row): zero them, so their zero weights add exactly zero
+        // whatever that was (0 * inf is not 0) ----
+#pragma unroll
+        for (int i = 0; i < NR; ++i)
+            if (w0 + i * C::RPL + rg >= seq) vr[i] = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
         for (int hh = 0; hh < HPK; ++hh)
 #pragma unroll
@@ -1116,31 +1126,51 @@ __global__ __launch_bounds__(64 * MfmaCfg<HPK>::WMAX) void attn_mfma_kernel(cwi:
     const int W = blockDim.x >> 6;
     const int CP = C::PW * W;
     const int c = blockIdx.x, g = blockIdx.y;
-    const int seq = a.pos_dev ? (*a.pos_dev + 1) : a.seq;
-    // a device-resident position past the cache (the host bounds the
-    // position it tracks; this covers a state it could not see): no KV
-    // row is written and nothing past the cache is read
-    if (seq < 1 || seq > a.max_seq) return;
     const int c0 = c * CP;
-    if (c0 >= seq) return;
-    const int n_chunks = (seq + CP - 1) / CP;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kv_dim = a.n_kv * HD;
-    const int pos_new = seq - 1;
     const int w0 = c0 + wave * C::PW;  // this wave's first position
-    const bool live = w0 < seq;        // (wave-uniform, like w_new)
-    const bool w_new = FUSED && pos_new >= w0 && pos_new < w0 + C::PW;
     unsigned char *kc = reinterpret_cast<unsigned char *>(a.k_cache);
     unsigned char *vc = reinterpret_cast<unsigned char *>(a.v_cache);
     const size_t row_bytes = (size_t)kv_dim * 2;
     const int lg = lane >> 4, li = lane & 15;  // lane group, lane in group
 
-    // ---- 1. loads, straight-line (see attn_wave_kernel), in the order they
-    // are used: a query head (waves below HPK), the new k and v (the wave
-    // holding pos_new), the K rows in the MFMA A layout (key li, bytes
-    // 64 lg + 16 t), then the V rows in their natural layout (rows 4 i + lg,
-    // 16-byte unit li); rows past the sequence clamp to its last row ----
+    // ---- 1. loads, straight-line (see attn_wave_kernel).  First the K rows
+    // in the MFMA A layout (key li, bytes 64 lg + 16 t) and the V rows in
+    // their natural layout (rows 4 i + lg, 16-byte unit li): their addresses
+    // do not depend on the device-resident position, so they are in flight
+    // while it is read (rows past the cache clamp to its last row; rows at
+    // or past the sequence are masked once it is known).  Then the position,
+    // and in the order they are used a query head (waves below HPK) and the
+    // new k and v with their RoPE row (the wave holding pos_new) ----
+    uint4 kr[4], vr[4];
+    {
+        int p = w0 + li;
+        p = p < a.max_seq ? p : a.max_seq - 1;
+        const unsigned char *src = kc + (size_t)p * row_bytes + (size_t)g * C::ROWB + lg * 64;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) kr[t] = *reinterpret_cast<const uint4 *>(src + 16 * t);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int p = w0 + 4 * i + lg;
+        p = p < a.max_seq ? p : a.max_seq - 1;
+        vr[i] = *reinterpret_cast<const uint4 *>(vc + (size_t)p * row_bytes +
+                                                (size_t)g * C::ROWB + (size_t)li * 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const int seq = a.pos_dev ? (*a.pos_dev + 1) : a.seq;
+    // a device-resident position past the cache (the host bounds the
+    // position it tracks; this covers a state it could not see): no KV
+    // row is written and nothing past the cache is read
+    if (seq < 1 || seq > a.max_seq) return;
+    if (c0 >= seq) return;
+    const int n_chunks = (seq + CP - 1) / CP;
+    const int pos_new = seq - 1;
+    const bool live = w0 < seq;  // (wave-uniform, like w_new)
+    const bool w_new = FUSED && pos_new >= w0 && pos_new < w0 + C::PW;
     const int h = g * HPK + (wave < HPK ? wave : HPK - 1);
     const bool q_wave = wave < HPK;
     auto rs = [](const float *p, bool use) {
@@ -1170,23 +1200,13 @@ __global__ __launch_bounds__(64 * MfmaCfg<HPK>::WMAX) void attn_mfma_kernel(cwi:
     } else {
         ld2(rs(a.q + (size_t)h * HD, q_wave), lo, hi);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    uint4 kr[4], vr[4];
-    {
-        int p = w0 + li;
-        p = p < seq ? p : seq - 1;
-        const unsigned char *src = kc + (size_t)p * row_bytes + (size_t)g * C::ROWB + lg * 64;
+    // V rows at or past the sequence hold whatever the cache holds there
+    // (zeros, or rows of an earlier sequence): zero them, so their zero
+    // weights add exactly zero whatever those rows were (0 * inf is not 0).
+    // Their scores are masked by position below.
 #pragma unroll
-        for (int t = 0; t < 4; ++t) kr[t] = *reinterpret_cast<const uint4 *>(src + 16 * t);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        int p = w0 + 4 * i + lg;
-        p = p < seq ? p : seq - 1;
-        vr[i] = *reinterpret_cast<const uint4 *>(vc + (size_t)p * row_bytes +
-                                                (size_t)g * C::ROWB + (size_t)li * 16);
-    }
+    for (int i = 0; i < 4; ++i)
+        if (w0 + 4 * i + lg >= seq) vr[i] = make_uint4(0u, 0u, 0u, 0u);
 
     // ---- 2. query head of waves below HPK (normalised + rotated when
     // fused), into LDS as f16 hi and lo parts ----

@@ -133,6 +133,44 @@ def test_fused_step_runs_after_the_layout_check(ctx):
     m.close()
 
 
+@pytest.mark.parametrize("kv_dtype", [cw.CW_F16, cw.CW_F32])
+def test_cache_rows_past_the_sequence_do_not_reach_the_output(ctx, kv_dtype):
+    """Attention reads the cache rows of its chunks before it knows the
+    device-resident position (the f16 kernel) or clamps them to the
+    sequence (the f32 one); either way rows at or past the sequence must not
+    reach the output, whatever they hold.  Two copies of one model: the
+    cache rows past the prompt hold NaN and inf in one and zeros in the
+    other; 8 replayed greedy steps and the logits of a step give the same
+    bits."""
+    P, N, max_seq = 40, 8, 96
+    cfg = cw.make_config(2, 256, 4, 2, 128, 512, 1000, max_seq, kv_dtype)
+    kv_dim = cfg.n_kv_heads * cfg.head_dim
+    dt = np.float16 if kv_dtype == cw.CW_F16 else np.float32
+    rng = np.random.default_rng(41)
+    k = rng.standard_normal((cfg.n_layers, max_seq, kv_dim)).astype(dt)
+    v = rng.standard_normal((cfg.n_layers, max_seq, kv_dim)).astype(dt)
+    k_bad, v_bad, k_zero, v_zero = k.copy(), v.copy(), k.copy(), v.copy()
+    k_bad[:, P:] = np.nan
+    v_bad[:, P:] = np.nan
+    v_bad[:, P + 1::3] = np.inf
+    k_zero[:, P:] = 0
+    v_zero[:, P:] = 0
+    out = []
+    for kk, vv in ((k_bad, v_bad), (k_zero, v_zero)):
+        m = cw.Model(ctx, cfg)
+        m.load_synthetic(77)
+        m.finalize()
+        m.prefill_kv(kk, vv, max_seq)
+        toks = m.generate(np.array([5], np.uint32), N, start_pos=P, mode=cw.STEP_GRAPH)
+        m.step(9, P + N)
+        out.append((toks, m.logits()))
+        m.close()
+    (t_bad, l_bad), (t_zero, l_zero) = out
+    assert np.all(np.isfinite(l_bad))
+    assert np.array_equal(t_bad, t_zero)
+    assert np.array_equal(l_bad.view(np.uint32), l_zero.view(np.uint32))
+
+
 def test_missing_tensor_is_an_error(ctx):
     cfg = cw.make_config(1, 64, 4, 2, 16, 128, 256, 8)
     m = cw.Model(ctx, cfg)
