@@ -1548,15 +1548,25 @@ AttnPick pick_wave_w(int hpk, int w, bool f) {
 
 // head_dim 128: the register-resident kernel, with W waves (16 positions
 // each) per workgroup: the largest W (at least the heads per kv head) whose
-// grid for a full cache still gives every CU a workgroup, else the smallest
+// grid for a full cache still gives every CU a workgroup.  When no W fills
+// the chip (small caches), W = 4: sequences up to 64 positions then need no
+// cross-workgroup merge, which at these sizes is most of the kernel (Qwen3-
+// 0.6B shape, 160-position f32 cache: 5.3 against 7.5 us per launch at 33
+// keys, 7.3 against 7.6 at 141; token loop 1492-1494 against 1475-1478
+// tokens/s; W = 8 was slower past 128 positions, 9.6 us)
 AttnPick pick_wave(const cw_ctx *ctx, int kv_dtype, int hpk, int n_kv, int max_seq, bool fused) {
     int w = 2;
+    bool fills = false;
     for (int cand : {8, 4, 2}) {
         if (cand < hpk) continue;
         w = cand;
         const long wgs = (long)((max_seq + 16 * cand - 1) / (16 * cand)) * n_kv;
-        if (wgs >= ctx->n_cu) break;
+        if (wgs >= ctx->n_cu) {
+            fills = true;
+            break;
+        }
     }
+    if (!fills) w = 4;
     if (w < hpk) w = hpk;
     return kv_dtype == CW_F16 ? pick_wave_w<_Float16>(hpk, w, fused)
                               : pick_wave_w<float>(hpk, w, fused);
