@@ -648,14 +648,14 @@ __global__ __launch_bounds__(64 * HPK) void attn_kernel(cwi::AttnArgs a, float s
 
 // Decode attention for head_dim 128 with the K/V rows kept in registers as
 // they were loaded: workgroup (chunk c, kv head g) has W waves, wave w owns
-// the PW = 16 positions c*CP + 16w ...  A lane holds, for NR rows of its
-// slice, one 16-byte unit of the row (EPU elements): the loads are plain
-// coalesced row reads, and no LDS tile or workgroup barrier sits between a
-// wave's data arriving and its compute, so each wave computes as soon as its
-// own rows are in.
+// the PW positions c*CP + PW*w ... (PW = 16, or 8 for small caches).  A
+// lane holds, for NR rows of its slice, one 16-byte unit of the row (EPU
+// elements): the loads are plain coalesced row reads, and no LDS tile or
+// workgroup barrier sits between a wave's data arriving and its compute, so
+// each wave computes as soon as its own rows are in.
 //   scores: per (row, head) a partial dot over the lane's EPU dims, summed
 //     over the U4_ROW lanes of the row with DPP (every lane gets the sum);
-//   softmax: per head over the wave's 16 positions;
+//   softmax: per head over the wave's PW positions;
 //   P.V: the lane's rows times their p, summed over the row groups;
 // the W wave partials meet in LDS; the workgroup writes one chunk partial
 // (or the output, for a single chunk) and the last workgroup of the kv head
@@ -677,7 +677,7 @@ __device__ __forceinline__ float row_group_sum(float v) {
     return v;
 }
 
-template <typename KVT, int HPK, int W>
+template <typename KVT, int HPK, int W, int PW_ = 16>
 struct WaveCfg {
     static constexpr int HD = 128;
     static constexpr int HALF = HD / 2;             // = 64: one (lo, hi) pair per lane
@@ -685,7 +685,7 @@ struct WaveCfg {
     static constexpr int EPU = 16 / ES;             // elements per 16-byte unit
     static constexpr int U4_ROW = HD / EPU;         // lanes per row: 16 (f16), 32 (f32)
     static constexpr int RPL = 64 / U4_ROW;         // rows per wave load
-    static constexpr int PW = 16;                   // positions per wave
+    static constexpr int PW = PW_;                  // positions per wave (16 or 8)
     static constexpr int NR = PW / RPL;             // rows per lane
     static constexpr int CP = PW * W;               // positions per workgroup
     static constexpr int THREADS = 64 * W;
@@ -754,10 +754,10 @@ __device__ __forceinline__ void lds_barrier() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-template <typename KVT, int HPK, int W, bool FUSED>
+template <typename KVT, int HPK, int W, bool FUSED, int PW = 16>
 __global__ __launch_bounds__(64 * W) void attn_wave_kernel(cwi::AttnArgs a, float scale,
                                                            int max_chunks) {
-    using C = WaveCfg<KVT, HPK, W>;
+    using C = WaveCfg<KVT, HPK, W, PW>;
     constexpr int HD = C::HD, HALF = C::HALF, EPU = C::EPU, NR = C::NR;
     extern __shared__ float lds_f[];
     float *q_s = lds_f;              // [HPK][HD]
@@ -1526,11 +1526,23 @@ AttnPick pick_attn(int kv_dtype, int hd, int hpk) {
     return kv_dtype == CW_F16 ? pick_hd<_Float16>(hd, hpk) : pick_hd<float>(hd, hpk);
 }
 
-template <typename KVT, int HPK, int W>
+template <typename KVT, int HPK, int W, int PW = 16>
 AttnPick make_wave_pick(bool fused) {
-    using C = WaveCfg<KVT, HPK, W>;
-    return {fused ? attn_wave_kernel<KVT, HPK, W, true> : attn_wave_kernel<KVT, HPK, W, false>,
+    using C = WaveCfg<KVT, HPK, W, PW>;
+    return {fused ? attn_wave_kernel<KVT, HPK, W, true, PW>
+                  : attn_wave_kernel<KVT, HPK, W, false, PW>,
             C::THREADS, C::CP, C::LDS};
+}
+
+// 8 waves of 8 positions: the small-cache f32 configuration
+AttnPick pick_wave_small_f32(int hpk, bool f) {
+    switch (hpk) {
+        case 1: return make_wave_pick<float, 1, 8, 8>(f);
+        case 2: return make_wave_pick<float, 2, 8, 8>(f);
+        case 4: return make_wave_pick<float, 4, 8, 8>(f);
+        case 8: return make_wave_pick<float, 8, 8, 8>(f);
+        default: return {nullptr, 0, 0, 0};
+    }
 }
 
 template <typename KVT>
@@ -1549,11 +1561,14 @@ AttnPick pick_wave_w(int hpk, int w, bool f) {
 // head_dim 128: the register-resident kernel, with W waves (16 positions
 // each) per workgroup: the largest W (at least the heads per kv head) whose
 // grid for a full cache still gives every CU a workgroup.  When no W fills
-// the chip (small caches), W = 4: sequences up to 64 positions then need no
-// cross-workgroup merge, which at these sizes is most of the kernel (Qwen3-
-// 0.6B shape, 160-position f32 cache: 5.3 against 7.5 us per launch at 33
-// keys, 7.3 against 7.6 at 141; token loop 1492-1494 against 1475-1478
-// tokens/s; W = 8 was slower past 128 positions, 9.6 us)
+// the chip (small caches), 64 positions per workgroup: sequences up to 64
+// positions then need no cross-workgroup merge, which at these sizes is most
+// of the kernel, and for f32 caches as 8 waves of 8 positions, which halves
+// each wave's chain of dependent reductions (Qwen3-0.6B shape, 160-position
+// f32 cache, per launch at 33 / 141 keys: 2 waves of 16, 7.5 / 7.6 us; 4 of
+// 16, 5.3 / 7.3; 8 of 8, 5.7 / 7.7 on another box, with the token loop at
+// 1498-1500 against 1485-1487 tokens/s for 4 of 16; 8 waves of 16 were
+// slower past 128 positions, 9.6 us)
 AttnPick pick_wave(const cw_ctx *ctx, int kv_dtype, int hpk, int n_kv, int max_seq, bool fused) {
     int w = 2;
     bool fills = false;
@@ -1566,6 +1581,7 @@ AttnPick pick_wave(const cw_ctx *ctx, int kv_dtype, int hpk, int n_kv, int max_s
             break;
         }
     }
+    if (!fills && kv_dtype == CW_F32) return pick_wave_small_f32(hpk, fused);
     if (!fills) w = 4;
     if (w < hpk) w = hpk;
     return kv_dtype == CW_F16 ? pick_wave_w<_Float16>(hpk, w, fused)
