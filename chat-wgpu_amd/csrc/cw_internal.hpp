@@ -210,6 +210,9 @@ struct GemvArgs {
     GenState *state;
     const uint32_t *prompt;
     uint32_t *tokens;
+    // waves of a workgroup that take wave tiles (0: all of them); set by
+    // launch_q4_gemv for launches too small to give every CU a workgroup
+    int tile_waves;
 };
 
 int launch_q4_gemv(cw_ctx *ctx, XSrc xs, Epi epi, const GemvArgs &a);
