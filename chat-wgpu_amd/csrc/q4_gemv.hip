@@ -227,9 +227,11 @@ __global__ __launch_bounds__(kThreads, 8) void q4_gemv_kernel(GemvArgs a, int n_
     const int rl = lane / G;
 
     // this wave's tiles: wv, wv + stride, ... (the first tile_waves waves of
-    // each workgroup take tiles; the others only stage the activation)
+    // each workgroup take tiles; the others only stage the activation, and
+    // their unused first loads re-read this workgroup's own last tile, in
+    // cache, not the next workgroup's)
     const int tw = a.tile_waves ? a.tile_waves : kWaves;
-    const int wv = blockIdx.x * tw + wave;
+    const int wv = blockIdx.x * tw + (wave < tw ? wave : tw - 1);
     const int stride = gridDim.x * tw;
     const int n_my = (wave < tw && wv < n_wave_tiles) ? (n_wave_tiles - 1 - wv) / stride + 1 : 0;
     const int total = n_my * S;
