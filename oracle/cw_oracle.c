@@ -27,7 +27,9 @@
  *   or_naive_matmul        closed form (ones -> k), f64 truth
  *   or_rmsnorm             main.rs:61-67 KAT, scale invariance, f64 truth
  *   or_rope_table/or_rope  main.rs:93-98 (pos 0 identity), norm preservation,
- *                          relative-position invariance, f32 literal formula
+ *                          relative-position invariance, f32 literal formula,
+ *                          rotation direction by one-hot inputs against
+ *                          numpy's cos/sin in rope.wgsl:30-31's signs
  *   or_attention           main.rs:100-118 (seq=1 -> V), constant-K mean,
  *                          f64 two-pass softmax
  *   or_swiglu / or_add     main.rs:77-82 and main.rs:154-161 KATs
