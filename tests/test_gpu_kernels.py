@@ -285,6 +285,9 @@ ATTN_CASES = [  # (n_heads, n_kv, hd, seq, f16)
     # the longest sequence an attention call takes (32768 positions), on
     # the 8B shape's heads
     (32, 8, 128, 32768, True), (32, 8, 128, 32768, False),
+    # the f16 kernel at 11 and 13 waves per workgroup (the wave count follows
+    # the cache length: 9 at 4097, 16 from about 7.7K)
+    (32, 8, 128, 5500, True), (32, 8, 128, 6500, True),
 ]
 
 
