@@ -126,7 +126,7 @@ int ctx_scratch(cw_ctx *ctx, size_t bytes, void **out) {
                 hipError_t e = hipStreamSynchronize(ctx->stream);
                 if (e == hipSuccess) e = hipFree(ctx->scratch);
                 if (e != hipSuccess) {
-                    hipFree(p);
+                    (void)hipFree(p);
                     return hip_fail(e, "ctx_scratch: releasing the old scratch", __FILE__, __LINE__);
                 }
             }
@@ -190,7 +190,7 @@ static hipEvent_t next_event(cw_ctx *ctx) {
 void prof_begin(cw_ctx *ctx, const char *label) {
     if (!ctx->profiling) return;
     cw_prof_rec r{next_event(ctx), nullptr, label};
-    if (r.start) hipEventRecord(r.start, ctx->stream);
+    if (r.start) (void)hipEventRecord(r.start, ctx->stream);
     ctx->prof.push_back(r);
 }
 
@@ -198,7 +198,7 @@ void prof_end(cw_ctx *ctx) {
     if (!ctx->profiling || ctx->prof.empty()) return;
     cw_prof_rec &r = ctx->prof.back();
     r.stop = next_event(ctx);
-    if (r.stop) hipEventRecord(r.stop, ctx->stream);
+    if (r.stop) (void)hipEventRecord(r.stop, ctx->stream);
 }
 
 void prof_events(cw_ctx *ctx, const char *label, hipEvent_t *start, hipEvent_t *stop) {
@@ -242,8 +242,8 @@ int cw_ctx_create(int device, cw_ctx **out) {
     if (e == hipSuccess) e = hipMemsetAsync(ctx->attn_cnt, 0, cnt_bytes, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) {
-        if (ctx->attn_cnt) hipFree(ctx->attn_cnt);
-        hipStreamDestroy(ctx->stream);
+        if (ctx->attn_cnt) (void)hipFree(ctx->attn_cnt);
+        (void)hipStreamDestroy(ctx->stream);
         delete ctx;
         return hip_fail(e, "attention counters", __FILE__, __LINE__);
     }
@@ -258,19 +258,19 @@ int cw_ctx_create(int device, cw_ctx **out) {
 
 int cw_ctx_destroy(cw_ctx *ctx) {
     if (!ctx) return CW_OK;
-    hipSetDevice(ctx->device);
-    hipStreamSynchronize(ctx->stream);
-    for (void *p : ctx->allocs) hipFree(p);
-    for (auto &c : ctx->chunks) hipFree(c.base);
-    if (ctx->scratch) hipFree(ctx->scratch);
-    for (void *p : ctx->scratch_retired) hipFree(p);
-    if (ctx->attn_cnt) hipFree(ctx->attn_cnt);
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    for (void *p : ctx->allocs) (void)hipFree(p);
+    for (auto &c : ctx->chunks) (void)hipFree(c.base);
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    for (void *p : ctx->scratch_retired) (void)hipFree(p);
+    if (ctx->attn_cnt) (void)hipFree(ctx->attn_cnt);
     for (auto &t : ctx->ropes) {
-        hipFree(t.cos_t);
-        hipFree(t.sin_t);
+        (void)hipFree(t.cos_t);
+        (void)hipFree(t.sin_t);
     }
-    for (hipEvent_t e : ctx->event_pool) hipEventDestroy(e);
-    hipStreamDestroy(ctx->stream);
+    for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
+    (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return CW_OK;
 }
@@ -447,13 +447,13 @@ int cw_graph_end(cw_ctx *ctx, cw_graph **out) {
     hipGraph_t graph = nullptr;
     hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
     if (e != hipSuccess) {
-        if (graph) hipGraphDestroy(graph);
+        if (graph) (void)hipGraphDestroy(graph);
         return hip_fail(e, "hipStreamEndCapture", __FILE__, __LINE__);
     }
     hipGraphExec_t exec = nullptr;
     e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
     if (e != hipSuccess) {
-        hipGraphDestroy(graph);
+        (void)hipGraphDestroy(graph);
         return hip_fail(e, "hipGraphInstantiate", __FILE__, __LINE__);
     }
     cw_graph *g = new cw_graph();
@@ -472,8 +472,8 @@ int cw_graph_launch(cw_ctx *ctx, const cw_graph *g) {
 
 int cw_graph_destroy(cw_graph *g) {
     if (!g) return CW_OK;
-    if (g->exec) hipGraphExecDestroy(g->exec);
-    if (g->graph) hipGraphDestroy(g->graph);
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
     delete g;
     return CW_OK;
 }

@@ -308,14 +308,14 @@ int ensure_graph(cw_model *m) {
     hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
     ctx->profiling = prof;
     if (rc != CW_OK) {
-        if (graph) hipGraphDestroy(graph);
+        if (graph) (void)hipGraphDestroy(graph);
         return rc;
     }
     if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture", __FILE__, __LINE__);
     hipGraphExec_t exec = nullptr;
     e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
     if (e != hipSuccess) {
-        hipGraphDestroy(graph);
+        (void)hipGraphDestroy(graph);
         return hip_fail(e, "hipGraphInstantiate", __FILE__, __LINE__);
     }
     m->graph = graph;
@@ -814,11 +814,11 @@ int cw_step_dry_plan(const cw_model_config *cfg, int n_cu, int split_gate_up, vo
 int cw_model_destroy(cw_model *m) {
     if (!m) return CW_OK;
     CW_TRY(refuse_recording(m, "cw_model_destroy"));
-    hipStreamSynchronize(m->ctx->stream);
-    if (m->graph_exec) hipGraphExecDestroy(m->graph_exec);
-    if (m->graph) hipGraphDestroy(m->graph);
-    for (void *p : m->allocs) hipFree(p);
-    for (void *p : m->pf_allocs) hipFree(p);
+    (void)hipStreamSynchronize(m->ctx->stream);
+    if (m->graph_exec) (void)hipGraphExecDestroy(m->graph_exec);
+    if (m->graph) (void)hipGraphDestroy(m->graph);
+    for (void *p : m->allocs) (void)hipFree(p);
+    for (void *p : m->pf_allocs) (void)hipFree(p);
     delete m;
     return CW_OK;
 }
@@ -1248,7 +1248,7 @@ int cw_model_profile_step(cw_model *m, int64_t *ticks, int max_n, int *n_out, do
         if (e == hipSuccess) e = hipStreamSynchronize(m->ctx->stream);
         if (e != hipSuccess) rc = hip_fail(e, "trace download", __FILE__, __LINE__);
     }
-    hipFree(dev);
+    (void)hipFree(dev);
     CW_TRY(rc);
     CW_TRY(check_fused(m));
     const int k = n < max_n ? n : max_n;
