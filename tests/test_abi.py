@@ -108,3 +108,43 @@ def test_synthetic_weights_cover_every_tensor():
     assert len(w) == 2 * 11 + 2
     s, q = w["blk.1.ffn_down.weight"]
     assert s.shape == (64, 4) and q.shape == (64, 4, 16)
+
+
+NULL_PROBE = r'''
+import sys
+sys.path.insert(0, sys.argv[1])
+import cw
+lib = cw.lib()
+for name, (res, args) in sorted(cw._SIGS.items()):
+    if res is not cw._I or not args:
+        continue
+    vals = [0.0 if a is cw._F else 0 if a in (cw._I, cw._U32, cw._SZ, cw._U64) else None
+            for a in args]
+    rc = getattr(lib, name)(*vals)
+    print(name, rc, lib.cw_last_error().decode(), flush=True)
+'''
+
+
+def test_every_entry_point_refuses_null_and_zero_arguments():
+    """Every int-returning entry point called with null handles and pointers
+    and zero sizes returns a status code, never crashes: CW_ERR_ARG with a
+    message naming the call, except the destroy/close calls (a null handle is
+    nothing to free) and cw_gguf_has (0: no such tensor).  Run in a child
+    process so that a crash would show as its exit status."""
+    import subprocess
+    import sys as _sys
+    r = subprocess.run([_sys.executable, "-c", NULL_PROBE, os.path.join(ROOT, "chat-wgpu_amd")],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    seen = 0
+    for line in r.stdout.splitlines():
+        name, rc, msg = line.split(" ", 2)
+        rc = int(rc)
+        seen += 1
+        if name in ("cw_ctx_destroy", "cw_model_destroy", "cw_gguf_close", "cw_graph_destroy",
+                    "cw_gguf_has"):
+            assert rc == 0, line
+        else:
+            assert rc == -1, line
+            assert msg.startswith(name + ":"), line
+    assert seen >= 70, r.stdout
